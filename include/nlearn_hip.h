@@ -1,0 +1,212 @@
+/*
+ * nlearn_hip.h — C ABI of the MI355X (gfx950) kernels behind nlearn's three
+ * training hot paths: causal FlashAttention (forward + recompute backward), the
+ * bf16 GEMM used by `linear`, and the fused softmax cross-entropy.
+ *
+ * Conventions shared by every entry point
+ *   - Plain C types only. `stream` is a hipStream_t passed as void* (NULL = the
+ *     default stream). Every call is stream-ordered and asynchronous: no host
+ *     synchronisation, no device allocation, no global mutable state.
+ *   - Tensors are device pointers. bf16 values are raw IEEE bfloat16 bit
+ *     patterns (nl_bf16 = uint16_t). All arithmetic inside the kernels is fp32.
+ *   - Matrices are row-major with an explicit leading dimension (elements
+ *     between consecutive rows). Row-major dense tensors pass ld = #columns.
+ *   - Return value: NL_OK (0) on success, otherwise an NL_E* code. Argument
+ *     errors are detected on the host before anything is launched; launch
+ *     failures report hipGetLastError. nl_last_error() gives a message for the
+ *     most recent failure on the calling thread.
+ *
+ * Reference interfaces replaced (paths relative to the nlearn repository):
+ *   jax.ffi target "flash_attention_fwd"       nlearn/attention.py:82-91
+ *   jax.ffi target "flash_attention_bwd_dq"    nlearn/attention.py:117-121
+ *   jax.ffi target "flash_attention_bwd_dkdv"  nlearn/attention.py:122-127
+ *   XLA D = sum(dO*O, -1)                      nlearn/attention.py:116
+ *   jax.ffi target "gemm" + _gemm_padded       nlearn/kernels/gemm.py:32-58
+ *   _gemm_bwd transposes                       nlearn/kernels/gemm.py:71-76
+ *   jax.ffi target "ce_fwd"                    nlearn/kernels/cross_entropy.py:28-36
+ *   jax.ffi target "ce_bwd"                    nlearn/kernels/cross_entropy.py:39-46
+ *   loss.mean() / g * dlogits                  nlearn/kernels/cross_entropy.py:51,65
+ */
+#ifndef NLEARN_HIP_H
+#define NLEARN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t nl_bf16;
+
+/* ---- status codes ------------------------------------------------------- */
+#define NL_OK           0
+#define NL_EINVAL       1  /* bad shape, size or enum argument              */
+#define NL_EALIGN       2  /* pointer or leading dimension misaligned       */
+#define NL_EUNSUPPORTED 3  /* valid request this build does not implement   */
+#define NL_ELAUNCH      4  /* kernel launch failed (hipGetLastError)        */
+
+const char* nl_strerror(int status);
+/* Message of the most recent failing call on this thread ("" if none). */
+const char* nl_last_error(void);
+/* Library version string, e.g. "nlearn_hip 0.1 gfx950". */
+const char* nl_version(void);
+
+/* ======================================================================== */
+/* GEMM                                                                      */
+/* ======================================================================== */
+/*
+ * C[M,N] = alpha * s * op(A)[M,K] . op(B)[K,N] + beta * C
+ *   s = *alpha_dev if alpha_dev != NULL, else 1 (a device-side scale factor,
+ *       used to fold an upstream cotangent into the product without a sync).
+ *   op(A) = A   stored [M][lda] (opA = NL_OP_N)   or
+ *         = A^T with A stored [K][lda] (opA = NL_OP_T);
+ *   op(B) = B   stored [K][ldb] (opB = NL_OP_N)   or
+ *         = B^T with B stored [N][ldb] (opB = NL_OP_T).
+ * A, B are bf16; the product accumulates in fp32; C is fp32 or bf16 (RNE).
+ * beta == 0 never reads C. Tails in M, N and K are handled in-kernel (no host
+ * padding). Requirements: A, B, C 16-byte aligned; lda, ldb, ldc multiples of
+ * 8; M, N, K >= 0 (an empty product with K == 0 writes beta*C).
+ *
+ * Replaces: gemm(A,B) -> f32 C (gemm.py:32-40, 61-64) with opA=opB=N;
+ *   dA = dC . B^T  (gemm.py:74) with opA=N, opB=T, no materialised transpose;
+ *   dB = A^T . dC  (gemm.py:75) with opA=T, opB=N, no materialised transpose.
+ */
+#define NL_OP_N 0
+#define NL_OP_T 1
+#define NL_DTYPE_F32  0
+#define NL_DTYPE_BF16 1
+
+int nl_gemm(void* stream, int opA, int opB, int M, int N, int K,
+            float alpha, const nl_bf16* A, int64_t lda,
+            const nl_bf16* B, int64_t ldb,
+            float beta, void* C, int c_dtype, int64_t ldc,
+            const float* alpha_dev);
+
+/* ======================================================================== */
+/* Causal FlashAttention (head dim 64)                                        */
+/* ======================================================================== */
+/*
+ * Strided layout of one attention operand: element (b, h, s, d) lives at
+ *   base + b*batch + h*head + s*row + d        (d is contiguous).
+ * The reference's contiguous (n, s, d) tensors are batch = s*d, head = 0 with
+ * heads = 1 (or any equivalent split of n). The strided form lets a caller
+ * hand over the fused QKV projection output [bs, s, 3*H*64] directly, with no
+ * head-folding transposes (model.py:173-198 does them in XLA).
+ * L and D are always dense fp32 [batch][heads][seq].
+ */
+typedef struct nl_attn_stride {
+  int64_t batch;
+  int64_t head;
+  int64_t row;
+} nl_attn_stride;
+
+/*
+ * O = softmax(scale * Q K^T + causal mask) V,  L = logsumexp row (natural log).
+ * Requires d_head == 64, seq >= 1 (any length; tails masked), strides multiples
+ * of 8 elements and 16-byte aligned bases. causal must be 1 (the reference path
+ * is causal-only, flash_attention.metal:107).
+ * Replaces "flash_attention_fwd" (attention.py:82-91, flash_attention.metal:55-146).
+ */
+int nl_flash_attention_fwd(void* stream, int batch, int heads, int seq, int d_head,
+                           float scale, int causal,
+                           const nl_bf16* Q, nl_attn_stride sq,
+                           const nl_bf16* K, nl_attn_stride sk,
+                           const nl_bf16* V, nl_attn_stride sv,
+                           nl_bf16* O, nl_attn_stride so,
+                           float* L);
+
+/* D[b,h,s] = sum_d dO * O  (fp32).  Replaces attention.py:116. */
+int nl_flash_attention_bwd_preprocess(void* stream, int batch, int heads, int seq,
+                                      int d_head,
+                                      const nl_bf16* O, nl_attn_stride so,
+                                      const nl_bf16* dO, nl_attn_stride sdo,
+                                      float* D);
+
+/* dQ = scale * dS K with dS = P o (dP - D), P recomputed from L.
+ * Replaces "flash_attention_bwd_dq" (attention.py:117-121,
+ * flash_attention.metal:168-243). */
+int nl_flash_attention_bwd_dq(void* stream, int batch, int heads, int seq, int d_head,
+                              float scale, int causal,
+                              const nl_bf16* Q, nl_attn_stride sq,
+                              const nl_bf16* K, nl_attn_stride sk,
+                              const nl_bf16* V, nl_attn_stride sv,
+                              const nl_bf16* dO, nl_attn_stride sdo,
+                              const float* L, const float* D,
+                              nl_bf16* dQ, nl_attn_stride sdq);
+
+/* dV = P^T dO, dK = scale * dS^T Q.
+ * Replaces "flash_attention_bwd_dkdv" (attention.py:122-127,
+ * flash_attention.metal:265-347). */
+int nl_flash_attention_bwd_dkdv(void* stream, int batch, int heads, int seq, int d_head,
+                                float scale, int causal,
+                                const nl_bf16* Q, nl_attn_stride sq,
+                                const nl_bf16* K, nl_attn_stride sk,
+                                const nl_bf16* V, nl_attn_stride sv,
+                                const nl_bf16* dO, nl_attn_stride sdo,
+                                const float* L, const float* D,
+                                nl_bf16* dK, nl_attn_stride sdk,
+                                nl_bf16* dV, nl_attn_stride sdv);
+
+/* Whole backward (preprocess + dK/dV + dQ) in one call. `ws` is a caller-owned
+ * device workspace of nl_flash_attention_bwd_ws_bytes() bytes (holds D).
+ * Replaces _flash_bwd_rule (attention.py:111-128). */
+size_t nl_flash_attention_bwd_ws_bytes(int batch, int heads, int seq);
+int nl_flash_attention_bwd(void* stream, int batch, int heads, int seq, int d_head,
+                           float scale, int causal,
+                           const nl_bf16* Q, nl_attn_stride sq,
+                           const nl_bf16* K, nl_attn_stride sk,
+                           const nl_bf16* V, nl_attn_stride sv,
+                           const nl_bf16* O, nl_attn_stride so,
+                           const nl_bf16* dO, nl_attn_stride sdo,
+                           const float* L,
+                           nl_bf16* dQ, nl_attn_stride sdq,
+                           nl_bf16* dK, nl_attn_stride sdk,
+                           nl_bf16* dV, nl_attn_stride sdv,
+                           void* ws);
+
+/* ======================================================================== */
+/* Softmax cross-entropy                                                      */
+/* ======================================================================== */
+/*
+ * logits: bf16 [M][ld_logits] (V valid columns); targets: int32 [M].
+ * A target outside [0, V) yields loss = NaN for that row (the reference kernel
+ * has no check and reads out of bounds, cross_entropy.metal:66).
+ */
+
+/* loss[m] = lse[m] - logits[m, t[m]],  lse[m] = logsumexp(logits[m]).
+ * Replaces "ce_fwd" (cross_entropy.py:28-36, cross_entropy.metal:38-68). */
+int nl_ce_fwd(void* stream, int M, int V,
+              const nl_bf16* logits, int64_t ld_logits, const int32_t* targets,
+              float* loss, float* lse);
+
+/* dlogits[m,v] = (exp(logits[m,v] - lse[m]) - [v == t[m]]) * scale  (bf16).
+ * The reference uses scale = 1/M. Replaces "ce_bwd" (cross_entropy.py:39-46,
+ * cross_entropy.metal:81-97). */
+int nl_ce_bwd(void* stream, int M, int V,
+              const nl_bf16* logits, int64_t ld_logits, const int32_t* targets,
+              const float* lse, float scale,
+              nl_bf16* dlogits, int64_t ld_dlogits);
+
+/* Single pass over the logits: loss, lse and dlogits together. dlogits may
+ * alias logits (then ld_dlogits must equal ld_logits) and is written in place.
+ * Fuses ce_fwd + ce_bwd (cross_entropy.py:55-65). */
+int nl_ce_fwd_bwd(void* stream, int M, int V,
+                  const nl_bf16* logits, int64_t ld_logits, const int32_t* targets,
+                  float* loss, float* lse, float scale,
+                  nl_bf16* dlogits, int64_t ld_dlogits);
+
+/* out[0] = mean(x[0..n)) in a fixed summation order (deterministic).
+ * Replaces loss.mean() (cross_entropy.py:51). */
+int nl_mean_f32(void* stream, const float* x, int n, float* out);
+
+/* x[r, c] *= *g for r < rows, c < cols (bf16, row stride ld). Reads the scalar
+ * on the device and returns without touching x when *g == 1, so the usual
+ * unit cotangent costs one tiny launch. Replaces g * dlogits (cross_entropy.py:65). */
+int nl_scale_bf16_by_device_scalar(void* stream, nl_bf16* x, int64_t rows, int64_t cols,
+                                   int64_t ld, const float* g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NLEARN_HIP_H */

@@ -1,0 +1,102 @@
+// common.h — shared device helpers and host-side status plumbing for the
+// gfx950 kernels. Everything here is CDNA4-specific: 64-lane wavefronts,
+// MFMA bf16 fragments, fp32 <-> bf16 conversions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string>
+
+#include "../../include/nlearn_hip.h"
+
+namespace nl {
+
+// ---------------------------------------------------------------------------
+// vector types
+// ---------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// bf16 <-> fp32
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_lo(uint32_t pair) { return __uint_as_float(pair << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t pair) { return __uint_as_float(pair & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN). gfx950 lowers the
+// __bf16 conversion to v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  __bf16 b = (__bf16)f;
+  return __builtin_bit_cast(uint16_t, b);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// exp2 / log2 on the transcendental unit (v_exp_f32 / v_log_f32).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------
+// wavefront reductions (butterfly over all 64 lanes)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers (gfx950 bf16, fp32 accumulate)
+//   32x32x16: a = 8 bf16 of row (lane%32), k = 8*(lane/32)..+7
+//             b = 8 bf16 of col (lane%32), same k
+//             d[r] = D[8*(r/4) + 4*(lane/32) + r%4][lane%32]
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+// 8x8 transpose of 16-bit elements held as 8 rows x 4 dwords.
+// in[r] holds row r: dword j = (col 2j, col 2j+1). out[c] holds column c:
+// dword j = (row 2j, row 2j+1). 32 v_perm_b32.
+__device__ __forceinline__ void transpose8x8_b16(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int dw = c >> 1;
+    // byte selectors: v_perm_b32(a, b, sel) picks bytes of {a, b} (b = bytes 0-3,
+    // a = bytes 4-7). Low halfword from row 2j (source b), high from row 2j+1 (a).
+    const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[c][j] = __builtin_amdgcn_perm(in[2 * j + 1][dw], in[2 * j][dw], sel);
+    }
+  }
+}
+
+}  // namespace nl
+
+// ---------------------------------------------------------------------------
+// host-side error plumbing (defined in api.hip)
+// ---------------------------------------------------------------------------
+int nl_set_error(int code, const std::string& msg);
+int nl_check_launch(const char* what);

@@ -1,0 +1,200 @@
+"""nlearn_amd.kernels.gemm — ``gemm``, ``matmul`` and ``linear`` on the gfx950 MFMA GEMM.
+
+Mirrors nlearn/kernels/gemm.py (same names, same argument meaning):
+
+* ``gemm(A, B)``      differentiable A[M,K] @ B[K,N] -> fp32 C (gemm.py:61-79);
+* ``matmul(A, B)``    drop-in for ``@`` on 2-D operands (gemm.py:82-90);
+* ``linear(x, W)``    x[..., K] @ W[K, N] as ONE flattened GEMM, output in
+                      x's dtype (gemm.py:93-115).
+
+Differences from the reference, all on purpose:
+
+* no host padding: the kernel masks M/N/K tails (gemm.py:47-58 padded to 32/64);
+* no materialised transposes in the backward: dA = dC.B^T and dB = A^T.dC are
+  the kernel's NT and TN forms (gemm.py:74-75 transposed in XLA);
+* ``linear`` writes bf16 straight from the fp32 accumulators (gemm.py:114 wrote
+  fp32 then cast), and its weight gradient is produced in fp32 for an fp32
+  master weight, so no bf16 rounding of the gradient;
+* there is no pure-framework fallback (gemm.py:115): the HIP library is
+  required, and a missing library raises.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+_BF16 = torch.bfloat16
+_F32 = torch.float32
+
+
+def _check_device(*ts):
+    for t in ts:
+        if not t.is_cuda:
+            raise RuntimeError("nlearn_amd kernels need HIP device tensors (got a CPU tensor)")
+
+
+def _ld(t: torch.Tensor) -> int:
+    """Leading dimension of a row-major 2-D view (unit column stride required)."""
+    if t.dim() != 2:
+        raise ValueError(f"expected a 2-D tensor, got shape {tuple(t.shape)}")
+    if t.stride(1) != 1 and t.shape[1] > 1:
+        raise ValueError("GEMM operands need a unit column stride")
+    return max(t.stride(0), t.shape[1]) if t.shape[0] > 1 else (t.shape[1] + 7) // 8 * 8
+
+
+def _aligned(t: torch.Tensor) -> bool:
+    return t.data_ptr() % 16 == 0 and _ld(t) % 8 == 0
+
+
+def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
+    """bf16, unit column stride, 16-byte aligned rows; copies only when it must."""
+    if t.dtype != _BF16:
+        t = t.to(_BF16)
+    if t.dim() == 2 and (t.stride(1) == 1 or t.shape[1] <= 1) and _aligned(t):
+        return t
+    rows, cols = t.shape
+    ld = (cols + 7) // 8 * 8
+    buf = torch.empty((rows, ld), dtype=_BF16, device=t.device)
+    view = buf[:, :cols]
+    view.copy_(t)
+    return view
+
+
+def padded_empty(rows: int, cols: int, dtype=_BF16, device="cuda") -> torch.Tensor:
+    """A [rows, cols] view whose rows start on 16-byte boundaries (ld rounded to 8)."""
+    ld = (cols + 7) // 8 * 8
+    return torch.empty((rows, ld), dtype=dtype, device=device)[:, :cols]
+
+
+def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", out_dtype=_F32,
+             out: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 0.0,
+             alpha_dev: torch.Tensor | None = None) -> torch.Tensor:
+    """C = alpha * [*alpha_dev] * op(A) @ op(B) + beta * C on the current stream.
+
+    opA == "T": A is stored [K, M]; opB == "T": B is stored [N, K].
+    """
+    _check_device(A, B)
+    A = _kernel_ready(A)
+    B = _kernel_ready(B)
+    M = A.shape[1] if opA == "T" else A.shape[0]
+    K = A.shape[0] if opA == "T" else A.shape[1]
+    Kb = B.shape[1] if opB == "T" else B.shape[0]
+    N = B.shape[0] if opB == "T" else B.shape[1]
+    if K != Kb:
+        raise ValueError(f"gemm: inner dimensions differ ({K} vs {Kb})")
+    if out is None:
+        if beta != 0.0:
+            raise ValueError("gemm: beta != 0 needs an output tensor")
+        out = padded_empty(M, N, out_dtype, A.device)
+    if out.dtype not in (_F32, _BF16):
+        raise ValueError("gemm: output must be float32 or bfloat16")
+    if tuple(out.shape) != (M, N):
+        raise ValueError(f"gemm: output shape {tuple(out.shape)} != {(M, N)}")
+    if alpha_dev is not None and (alpha_dev.dtype != _F32 or not alpha_dev.is_cuda):
+        raise ValueError("gemm: alpha_dev must be a float32 device scalar")
+    stream = torch.cuda.current_stream(A.device).cuda_stream
+    _lib.call("nl_gemm", stream, _lib.NL_OP_T if opA == "T" else _lib.NL_OP_N,
+              _lib.NL_OP_T if opB == "T" else _lib.NL_OP_N, M, N, K, float(alpha),
+              A.data_ptr(), _ld(A), B.data_ptr(), _ld(B), float(beta), out.data_ptr(),
+              _lib.NL_DTYPE_F32 if out.dtype == _F32 else _lib.NL_DTYPE_BF16, _ld(out),
+              alpha_dev.data_ptr() if alpha_dev is not None else None)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# bf16 shadows of fp32 weights (model.py:372-375 casts every parameter each step)
+# ---------------------------------------------------------------------------
+
+
+def bf16_shadow(W: torch.Tensor) -> torch.Tensor:
+    """The bf16 copy of an fp32 weight, refreshed only when the weight changed.
+
+    An optimizer that writes the bf16 copy itself (the fused AdamW) tags it with
+    the weight's version counter so this returns it without another cast.
+    """
+    if W.dtype == _BF16:
+        return W
+    sh = getattr(W, "_nl_bf16", None)
+    if sh is not None and getattr(W, "_nl_bf16_version", None) == W._version:
+        return sh
+    sh = _kernel_ready(W.detach())
+    if sh.data_ptr() == W.data_ptr():  # pragma: no cover - dtype differs, cannot alias
+        sh = sh.clone()
+    W._nl_bf16 = sh
+    W._nl_bf16_version = W._version
+    return sh
+
+
+# ---------------------------------------------------------------------------
+# gemm — gemm.py:61-79
+# ---------------------------------------------------------------------------
+
+
+class _Gemm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, A, B):
+        ctx.save_for_backward(A, B)
+        return gemm_raw(A, B, out_dtype=_F32)
+
+    @staticmethod
+    def backward(ctx, dC):
+        A, B = ctx.saved_tensors
+        dA = dB = None
+        if ctx.needs_input_grad[0]:
+            dA = gemm_raw(dC, B, "N", "T", out_dtype=_F32).to(A.dtype)   # dC . B^T
+        if ctx.needs_input_grad[1]:
+            dB = gemm_raw(A, dC, "T", "N", out_dtype=_F32).to(B.dtype)   # A^T . dC
+        return dA, dB
+
+
+def gemm(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """Differentiable A[M,K] @ B[K,N] -> C[M,N] (fp32), bf16 operands."""
+    return _Gemm.apply(A, B)
+
+
+def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
+    """``A @ B`` on the HIP GEMM. 2-D x 2-D is one kernel; a leading batch of A
+    ([..., M, K] @ [K, N]) is flattened into M. Other shapes are rejected."""
+    if A.dim() == 2 and B.dim() == 2:
+        return gemm(A, B)
+    if A.dim() > 2 and B.dim() == 2:
+        lead = A.shape[:-1]
+        return gemm(A.reshape(-1, A.shape[-1]), B).reshape(*lead, B.shape[1])
+    raise ValueError(f"matmul: unsupported operand ranks {A.dim()} and {B.dim()}")
+
+
+# ---------------------------------------------------------------------------
+# linear — gemm.py:93-115
+# ---------------------------------------------------------------------------
+
+
+class _Linear(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x2, W):
+        Wb = bf16_shadow(W)
+        out_dtype = x2.dtype if x2.dtype in (_BF16, _F32) else _F32
+        y = gemm_raw(x2, Wb, out_dtype=out_dtype)
+        ctx.save_for_backward(x2, W)
+        ctx.wb = Wb
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, W = ctx.saved_tensors
+        Wb = ctx.wb
+        dx = dW = None
+        if ctx.needs_input_grad[0]:
+            dx = gemm_raw(dy, Wb, "N", "T", out_dtype=x2.dtype)             # dY . W^T
+        if ctx.needs_input_grad[1]:
+            dW = gemm_raw(x2, dy, "T", "N", out_dtype=_F32 if W.dtype == _F32 else W.dtype)  # X^T . dY
+        return dx, dW
+
+
+def linear(x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
+    """x[..., K] @ W[K, N] -> [..., N] in x's dtype, as one GEMM with M = prod(lead)."""
+    if x.dim() < 2 or W.dim() != 2:
+        raise ValueError("linear: x needs >= 2 dims and W exactly 2")
+    lead = x.shape[:-1]
+    y = _Linear.apply(x.reshape(-1, x.shape[-1]), W)
+    return y.reshape(*lead, W.shape[1])

@@ -1,0 +1,134 @@
+"""Float64 NumPy restatement of the three hot-path ops. TEST INFRASTRUCTURE ONLY.
+
+Each function cites the reference lines it restates (paths relative to the
+nlearn repository).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+# ---------------------------------------------------------------------------
+# bfloat16
+# ---------------------------------------------------------------------------
+
+
+def bf16_bits(x) -> np.ndarray:
+    """float -> bfloat16 bit patterns (uint16), round-to-nearest-even; NaN -> quiet NaN.
+
+    The reference casts operands to bf16 before its kernels (gemm.py:51-52,
+    model.py:372-375); this is that cast.
+    """
+    f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
+    u = f.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(f)
+    lsb = (u >> 16) & 1
+    r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
+    r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+    return r.astype(np.uint16)
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def bf16_round(x) -> np.ndarray:
+    """Round to bf16 and back to float32."""
+    return bf16_to_f32(bf16_bits(x))
+
+
+# ---------------------------------------------------------------------------
+# GEMM — gemm.py:43-79, gemm.metal:48-115
+# ---------------------------------------------------------------------------
+
+
+def gemm(A, B, opA: str = "N", opB: str = "N") -> np.ndarray:
+    """op(A) @ op(B) in float64 on bf16-rounded operands.
+
+    opA = "T" means A is stored [K, M] and used transposed (dB = A^T dC,
+    gemm.py:75); opB = "T" means B is stored [N, K] (dA = dC B^T, gemm.py:74).
+    """
+    a = bf16_round(A).astype(np.float64)
+    b = bf16_round(B).astype(np.float64)
+    if opA == "T":
+        a = a.T
+    if opB == "T":
+        b = b.T
+    return a @ b
+
+
+# ---------------------------------------------------------------------------
+# causal attention — attention.py:138-156 (forward), flash_attention.metal:55-146
+# (L = max + log sum exp), validate_flash_bwd.py:31-38 (analytic backward)
+# ---------------------------------------------------------------------------
+
+
+def _scale(d: int, scale):
+    return 1.0 / np.sqrt(d) if scale is None else float(scale)
+
+
+def flash_fwd(Q, K, V, scale=None, causal: bool = True):
+    """O = softmax(scale Q K^T + mask) V and L = logsumexp of each score row.
+
+    Q, K, V: (n, s, d). Returns O (n, s, d) and L (n, s), float64.
+    """
+    Q = np.asarray(Q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    n, s, d = Q.shape
+    sc = _scale(d, scale)
+    S = np.einsum("nqd,nkd->nqk", Q, K) * sc
+    if causal:
+        mask = np.triu(np.ones((s, s), bool), 1)
+        S = np.where(mask[None], -np.inf, S)
+    m = S.max(-1, keepdims=True)
+    e = np.exp(S - m)
+    l = e.sum(-1, keepdims=True)
+    P = e / l
+    O = np.einsum("nqk,nkd->nqd", P, V)
+    L = (m + np.log(l))[..., 0]
+    return O, L
+
+
+def flash_bwd(Q, K, V, dO, scale=None, causal: bool = True):
+    """dQ, dK, dV of sum(O * dO) with P recomputed from L, plus D = rowsum(dO * O).
+
+    dV = P^T dO; dP = dO V^T; dS = P (dP - D); dQ = scale dS K; dK = scale dS^T Q
+    (validate_flash_bwd.py:31-38; D as attention.py:116).
+    """
+    Q = np.asarray(Q, np.float64)
+    K = np.asarray(K, np.float64)
+    V = np.asarray(V, np.float64)
+    dO = np.asarray(dO, np.float64)
+    n, s, d = Q.shape
+    sc = _scale(d, scale)
+    O, L = flash_fwd(Q, K, V, sc, causal)
+    S = np.einsum("nqd,nkd->nqk", Q, K) * sc
+    P = np.exp(S - L[..., None])
+    if causal:
+        P = np.where(np.triu(np.ones((s, s), bool), 1)[None], 0.0, P)
+    D = np.einsum("nqd,nqd->nq", dO, O)
+    dV = np.einsum("nqk,nqd->nkd", P, dO)
+    dP = np.einsum("nqd,nkd->nqk", dO, V)
+    dS = P * (dP - D[..., None])
+    dQ = np.einsum("nqk,nkd->nqd", dS, K) * sc
+    dK = np.einsum("nqk,nqd->nkd", dS, Q) * sc
+    return dQ, dK, dV, D
+
+
+# ---------------------------------------------------------------------------
+# cross-entropy — cross_entropy.py:49-81, cross_entropy.metal:38-97
+# ---------------------------------------------------------------------------
+
+
+def ce(logits, targets, scale=None):
+    """Per-row loss, lse and dlogits = (softmax - onehot) * scale (default 1/M)."""
+    x = np.asarray(logits, np.float64)
+    t = np.asarray(targets, np.int64)
+    M, V = x.shape
+    m = x.max(-1, keepdims=True)
+    lse = (m + np.log(np.exp(x - m).sum(-1, keepdims=True)))[:, 0]
+    loss = lse - x[np.arange(M), t]
+    sc = (1.0 / M) if scale is None else float(scale)
+    dl = np.exp(x - lse[:, None])
+    dl[np.arange(M), t] -= 1.0
+    return loss, lse, dl * sc

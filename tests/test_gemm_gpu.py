@@ -1,0 +1,130 @@
+"""GPU parity of the MFMA GEMM (NN forward, NT dX, TN dW) against the oracle.
+
+Tolerance (north_star): relative L2 <= 5e-3 (fp32 accumulation); integer-valued
+inputs whose partial sums stay below 2^24 must match exactly.
+"""
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, rel_l2
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev_bf16(a, dev):
+    import torch
+
+    bits = ops.bf16_bits(a) if a.dtype != np.uint16 else a
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _np(t):
+    import torch
+
+    if t.dtype == torch.bfloat16:
+        return ops.bf16_to_f32(t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+    return t.contiguous().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["gemm_small", "gemm_medium", "gemm_large_magnitude"])
+def test_gemm_golden(dev, name):
+    import torch
+    from nlearn_amd.kernels.gemm import gemm_raw
+
+    g = np.load(GOLDEN / f"{name}.npz")
+    C = gemm_raw(_dev_bf16(g["A"], dev), _dev_bf16(g["B"], dev))
+    torch.cuda.synchronize()
+    assert rel_l2(_np(C), g["C"]) <= 5e-3
+
+
+@pytest.mark.parametrize("opA,opB", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (7, 9, 13), (32, 32, 16), (100, 130, 70), (257, 255, 129),
+                                   (300, 520, 1000), (64, 50257, 64), (513, 200, 50257)])
+def test_gemm_layouts_exact_small_integers(dev, opA, opB, M, N, K):
+    """Small integers: every product and partial sum is exact in fp32."""
+    import torch
+    from nlearn_amd.kernels.gemm import gemm_raw
+
+    rng = np.random.default_rng(M + 7 * N + 13 * K)
+    A = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, (K, N)).astype(np.float32)
+    As = A.T.copy() if opA == "T" else A
+    Bs = B.T.copy() if opB == "T" else B
+    ref = ops.gemm(As, Bs, opA, opB)
+    C = gemm_raw(_dev_bf16(As, dev), _dev_bf16(Bs, dev), opA, opB)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np(C), ref)
+
+
+@pytest.mark.parametrize("opA,opB", [("N", "N"), ("N", "T"), ("T", "N")])
+def test_gemm_bf16_out_alpha_beta_and_device_scale(dev, opA, opB):
+    import torch
+    from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
+
+    rng = np.random.default_rng(11)
+    M, N, K = 300, 200, 96
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    As = A.T.copy() if opA == "T" else A
+    Bs = B.T.copy() if opB == "T" else B
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    out = padded_empty(M, N, torch.float32, dev)
+    out.copy_(torch.from_numpy(C0))
+    s = torch.tensor(0.5, device=dev)
+    gemm_raw(_dev_bf16(As, dev), _dev_bf16(Bs, dev), opA, opB, out=out, alpha=2.0, beta=-1.0, alpha_dev=s)
+    ref = 1.0 * ops.gemm(As, Bs, opA, opB) - C0
+    torch.cuda.synchronize()
+    assert rel_l2(_np(out), ref) <= 5e-3
+    ob = gemm_raw(_dev_bf16(As, dev), _dev_bf16(Bs, dev), opA, opB, out_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert rel_l2(_np(ob), ops.gemm(As, Bs, opA, opB)) <= 5e-3
+
+
+@pytest.mark.parametrize("K,N", [(512, 1536), (512, 512), (512, 2048), (2048, 512), (512, 50257)])
+def test_gemm_model_shapes(dev, K, N):
+    """M = 16384 (bs32 x seq512): forward, dX = dY W^T and dW = X^T dY, checked on
+    sampled rows / columns against the float64 oracle."""
+    import torch
+    from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
+
+    M = 16384
+    gen = torch.Generator(device=dev).manual_seed(K + N)
+    X = torch.randn((M, K), generator=gen, device=dev).to(torch.bfloat16)
+    W = padded_empty(K, N, torch.bfloat16, dev)
+    W.copy_(torch.randn((K, N), generator=gen, device=dev) * 0.02)
+    dY = padded_empty(M, N, torch.bfloat16, dev)
+    dY.copy_(torch.randn((M, N), generator=gen, device=dev))
+    Y = gemm_raw(X, W, out_dtype=torch.bfloat16)
+    dX = gemm_raw(dY, W, "N", "T", out_dtype=torch.bfloat16)
+    dW = gemm_raw(X, dY, "T", "N", out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(0)
+    rows = rng.choice(M, 48, replace=False)
+    cols = rng.choice(N, 48, replace=False)
+    Xn, Wn = _np(X), _np(W)
+    rows_t = torch.from_numpy(rows).to(dev)
+    cols_t = torch.from_numpy(cols).to(dev)
+    assert rel_l2(_np(Y[rows_t]), ops.gemm(Xn[rows], Wn)) <= 5e-3
+    assert rel_l2(_np(dX[rows_t]), ops.gemm(_np(dY[rows_t]), Wn, "N", "T")) <= 5e-3
+    assert rel_l2(_np(dW[:, cols_t]), ops.gemm(Xn, _np(dY[:, cols_t]), "T", "N")) <= 5e-3
+
+
+def test_linear_autograd(dev):
+    import torch
+    from nlearn_amd.kernels.gemm import linear
+
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(ops.bf16_round(rng.standard_normal((4, 33, 64)).astype(np.float32))).to(dev)
+    W = torch.from_numpy((rng.standard_normal((64, 72)) * 0.1).astype(np.float32)).to(dev)
+    xb = x.to(torch.bfloat16).requires_grad_(True)
+    Wp = W.clone().requires_grad_(True)
+    y = linear(xb, Wp)
+    assert y.dtype == torch.bfloat16 and y.shape == (4, 33, 72)
+    gy = torch.from_numpy(ops.bf16_round(rng.standard_normal((4, 33, 72)).astype(np.float32))).to(dev)
+    y.backward(gy.to(torch.bfloat16))
+    xn, Wn, gn = x.cpu().numpy().reshape(-1, 64), W.cpu().numpy(), gy.cpu().numpy().reshape(-1, 72)
+    assert rel_l2(_np(y).reshape(-1, 72), ops.gemm(xn, Wn)) <= 5e-3
+    assert rel_l2(_np(xb.grad).reshape(-1, 64), ops.gemm(gn, Wn, "N", "T")) <= 5e-3
+    assert Wp.grad.dtype == torch.float32
+    assert rel_l2(Wp.grad.cpu().numpy(), ops.gemm(xn, gn, "T", "N")) <= 5e-3

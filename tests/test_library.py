@@ -1,0 +1,53 @@
+"""CPU checks of the C-ABI library: it builds for gfx950, loads, and exports
+every entry point declared in include/nlearn_hip.h (no GPU calls)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nlearn_hip.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nl_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    from nlearn_amd import _lib
+
+    lib = _lib.load()
+    names = header_functions()
+    assert len(names) >= 15
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+    # the ctypes table covers exactly the header
+    assert sorted(_lib.EXPORTED) == names
+
+
+def test_status_strings_and_argument_errors_without_gpu():
+    from nlearn_amd import _lib
+
+    lib = _lib.load()
+    assert lib.nl_strerror(_lib.NL_EALIGN) == b"misaligned pointer or leading dimension"
+    assert lib.nl_version().startswith(b"nlearn_hip")
+    # host-side validation runs before any HIP call
+    rc = lib.nl_gemm(None, 7, 0, 4, 4, 4, 1.0, None, 8, None, 8, 0.0, None, 0, 8, None)
+    assert rc == _lib.NL_EINVAL
+    assert b"opA" in lib.nl_last_error()
+    rc = lib.nl_gemm(None, 0, 0, 4, 4, 4, 1.0, 16, 6, 32, 8, 0.0, 48, 0, 8, None)
+    assert rc == _lib.NL_EALIGN
+    rc = lib.nl_ce_fwd(None, 4, 0, None, 8, None, None, None)
+    assert rc == _lib.NL_EINVAL
+    with pytest.raises(_lib.NlError):
+        _lib.call("nl_mean_f32", None, None, -1, None)
+
+
+def test_library_targets_gfx950_only():
+    from nlearn_amd import _build
+
+    assert "--offload-arch=gfx950" in _build.HIPCC_FLAGS
+    assert sum(f.startswith("--offload-arch") for f in _build.HIPCC_FLAGS) == 1
