@@ -28,9 +28,12 @@ def dev():
     return torch.device("cuda:0")
 
 
-def rel_l2(a, b):
+def rel_l2(a, b, floor=0.0):
+    """||a - b|| / max(||b||, floor * sqrt(b.size)). The floor keeps the ratio
+    meaningful when the exact answer is (close to) zero."""
     import numpy as np
 
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
-    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+    den = max(np.linalg.norm(b), floor * np.sqrt(max(b.size, 1)), 1e-300)
+    return float(np.linalg.norm(a - b) / den)

@@ -1,0 +1,182 @@
+"""GPU parity of the causal FlashAttention kernels against the float64 oracle.
+
+Tolerance (north_star): relative L2 <= 2e-2 for O, dQ, dK, dV; L (logsumexp)
+absolute <= 1e-2.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import GOLDEN, rel_l2
+from oracle import ops
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _dev_bf16(bits, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _np(t):
+    import torch
+
+    if t.dtype == torch.bfloat16:
+        return ops.bf16_to_f32(t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16))
+    return t.contiguous().cpu().numpy()
+
+
+@pytest.mark.parametrize("name", ["flash_s1_2x128x64", "flash_s2_2x128x64"])
+def test_flash_golden(dev, name):
+    import torch
+    from nlearn_amd.attention import _flash_fwd_raw, flash_bwd_raw4
+
+    g = np.load(GOLDEN / f"{name}.npz")
+    Q, K, V, dO = (_dev_bf16(g[k], dev) for k in ("Q", "K", "V", "dO"))
+    O, L = _flash_fwd_raw(Q, K, V)
+    dq, dk, dv = flash_bwd_raw4(Q[:, None], K[:, None], V[:, None], O[:, None], dO[:, None], L[:, None])
+    torch.cuda.synchronize()
+    assert rel_l2(_np(O), g["O"]) <= TOL
+    assert np.abs(_np(L) - g["L"]).max() <= 1e-2
+    assert rel_l2(_np(dq[:, 0]), g["dQ"]) <= TOL
+    assert rel_l2(_np(dk[:, 0]), g["dK"]) <= TOL
+    assert rel_l2(_np(dv[:, 0]), g["dV"]) <= TOL
+
+
+def _rand_case(dev, B, H, S, seed, scale=1.0):
+    import torch
+
+    rng = np.random.default_rng(seed)
+    arrs = [ops.bf16_bits((rng.standard_normal((B, H, S, 64)) * scale).astype(np.float32)) for _ in range(4)]
+    dev_t = [_dev_bf16(a, dev) for a in arrs]
+    f32 = [ops.bf16_to_f32(a) for a in arrs]
+    return dev_t, f32
+
+
+def _check_against_oracle(outs, f32, B, H, S, causal=True):
+    O, L, dq, dk, dv = (_np(t) for t in outs)
+    q, k, v, do = (a.reshape(B * H, S, 64) for a in f32)
+    rO, rL = ops.flash_fwd(q, k, v, causal=causal)
+    rdq, rdk, rdv, _ = ops.flash_bwd(q, k, v, do, causal=causal)
+    assert rel_l2(O.reshape(B * H, S, 64), rO) <= TOL
+    assert np.abs(L.reshape(B * H, S) - rL).max() <= 1e-2
+    # with one key per query (S = 1) dQ and dK are exactly zero: floor the norm
+    assert rel_l2(dq.reshape(B * H, S, 64), rdq, floor=1e-3) <= TOL
+    assert rel_l2(dk.reshape(B * H, S, 64), rdk, floor=1e-3) <= TOL
+    assert rel_l2(dv.reshape(B * H, S, 64), rdv) <= TOL
+
+
+@pytest.mark.parametrize("B,H,S", [(1, 1, 1), (1, 2, 7), (2, 1, 64), (1, 3, 100), (2, 2, 129), (1, 1, 200),
+                                   (1, 2, 545)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_ragged_sequences(dev, B, H, S, causal):
+    import torch
+    from nlearn_amd.attention import flash_bwd_raw4, flash_fwd_raw4
+
+    (q, k, v, do), f32 = _rand_case(dev, B, H, S, seed=B * 100 + H * 10 + S)
+    O, L = flash_fwd_raw4(q, k, v, causal=causal)
+    dq, dk, dv = flash_bwd_raw4(q, k, v, O, do, L, causal=causal)
+    torch.cuda.synchronize()
+    _check_against_oracle((O, L, dq, dk, dv), f32, B, H, S, causal)
+
+
+def test_flash_fused_qkv_layout_and_autograd(dev):
+    """qkv (B, S, 3, H, D) consumed in place; O comes back as (B, S, H*D); the
+    backward writes one (B, S, 3, H, D) gradient."""
+    import torch
+    from nlearn_amd.attention import flash_attention_qkv
+
+    B, S, H = 2, 160, 3
+    rng = np.random.default_rng(9)
+    qkv_bits = ops.bf16_bits(rng.standard_normal((B, S, 3, H, 64)).astype(np.float32))
+    do_bits = ops.bf16_bits(rng.standard_normal((B, S, H * 64)).astype(np.float32))
+    qkv = _dev_bf16(qkv_bits, dev).requires_grad_(True)
+    out = flash_attention_qkv(qkv)
+    assert out.shape == (B, S, H * 64)
+    out.backward(_dev_bf16(do_bits, dev))
+    torch.cuda.synchronize()
+    x = ops.bf16_to_f32(qkv_bits)
+    q, k, v = (x[:, :, i].transpose(0, 2, 1, 3).reshape(B * H, S, 64) for i in range(3))
+    do = ops.bf16_to_f32(do_bits).reshape(B, S, H, 64).transpose(0, 2, 1, 3).reshape(B * H, S, 64)
+    rO, _ = ops.flash_fwd(q, k, v)
+    rdq, rdk, rdv, _ = ops.flash_bwd(q, k, v, do)
+    O = _np(out).reshape(B, S, H, 64).transpose(0, 2, 1, 3).reshape(B * H, S, 64)
+    assert rel_l2(O, rO) <= TOL
+    g = _np(qkv.grad)
+    for i, ref in enumerate((rdq, rdk, rdv)):
+        got = g[:, :, i].transpose(0, 2, 1, 3).reshape(B * H, S, 64)
+        assert rel_l2(got, ref) <= TOL
+
+
+def test_flash_reference_api_autograd(dev):
+    import torch
+    from nlearn_amd.attention import attention
+
+    n, S = 4, 96
+    rng = np.random.default_rng(4)
+    bits = [ops.bf16_bits(rng.standard_normal((n, S, 64)).astype(np.float32)) for _ in range(4)]
+    Q, K, V = (_dev_bf16(b, dev).requires_grad_(True) for b in bits[:3])
+    O = attention(Q, K, V)
+    O.backward(_dev_bf16(bits[3], dev))
+    q, k, v, do = (ops.bf16_to_f32(b) for b in bits)
+    rO, _ = ops.flash_fwd(q, k, v)
+    rdq, rdk, rdv, _ = ops.flash_bwd(q, k, v, do)
+    assert rel_l2(_np(O), rO) <= TOL
+    assert rel_l2(_np(Q.grad), rdq) <= TOL
+    assert rel_l2(_np(K.grad), rdk) <= TOL
+    assert rel_l2(_np(V.grad), rdv) <= TOL
+
+
+def test_flash_never_reads_beyond_causal_blocks(dev):
+    """Keys/values at positions >= 128 are poisoned with NaN: the first 128
+    queries' outputs (and the dQ of those queries) must be unchanged."""
+    import torch
+    from nlearn_amd.attention import flash_bwd_raw4, flash_fwd_raw4
+
+    (q, k, v, do), _ = _rand_case(dev, 1, 2, 256, seed=77)
+    O1, L1 = flash_fwd_raw4(q, k, v)
+    dq1, _, _ = flash_bwd_raw4(q, k, v, O1, do, L1)
+    k2, v2 = k.clone(), v.clone()
+    k2[:, :, 128:] = float("nan")
+    v2[:, :, 128:] = float("nan")
+    O2, L2 = flash_fwd_raw4(q, k2, v2)
+    do2 = do.clone()
+    do2[:, :, 128:] = 0
+    dq2, _, _ = flash_bwd_raw4(q, k2, v2, O2, do2, L2)
+    torch.cuda.synchronize()
+    assert torch.equal(O1[:, :, :128], O2[:, :, :128])
+    assert torch.equal(L1[:, :, :128], L2[:, :, :128])
+    assert torch.equal(dq1[:, :, :128], dq2[:, :, :128])
+
+
+@pytest.mark.parametrize("n,S", [(256, 512), (32, 4096)])
+def test_flash_baseline_shapes(dev, n, S):
+    """BASELINE flash configs: sampled heads vs the oracle, and on every head the
+    size-independent identities sum_j dV_j = sum_i dO_i and sum_j dK_j = 0."""
+    import torch
+    from nlearn_amd.attention import flash_bwd_raw4, flash_fwd_raw4
+
+    gen = torch.Generator(device=dev).manual_seed(n + S)
+    q, k, v, do = (torch.randn((n, 1, S, 64), generator=gen, device=dev).to(torch.bfloat16) for _ in range(4))
+    O, L = flash_fwd_raw4(q, k, v)
+    dq, dk, dv = flash_bwd_raw4(q, k, v, O, do, L)
+    torch.cuda.synchronize()
+    heads = [0, n // 2, n - 1]
+    ht = torch.tensor(heads, device=dev)
+    f = [_np(t[ht, 0]) for t in (q, k, v, do)]
+    rO, rL = ops.flash_fwd(*f[:3])
+    rdq, rdk, rdv, _ = ops.flash_bwd(*f)
+    assert rel_l2(_np(O[ht, 0]), rO) <= TOL
+    assert np.abs(_np(L[ht, 0]) - rL).max() <= 1e-2
+    assert rel_l2(_np(dq[ht, 0]), rdq) <= TOL
+    assert rel_l2(_np(dk[ht, 0]), rdk) <= TOL
+    assert rel_l2(_np(dv[ht, 0]), rdv) <= TOL
+    sdv = dv.float().sum(2)
+    sdo = do.float().sum(2)
+    assert ((sdv - sdo).norm() / sdo.norm()).item() < 2e-2
+    sdk = dk.float().sum(2)
+    assert (sdk.norm() / (dk.float().norm() * math.sqrt(S))).item() < 2e-2
+    assert torch.isfinite(O.float()).all() and torch.isfinite(dq.float()).all()
