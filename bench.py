@@ -1,0 +1,232 @@
+"""bench.py — training throughput of the BASELINE model on one MI355X.
+
+Workload (the metric's configuration): one full
+training step = forward + backward + AdamW of the d512/8h/4L/seq512 model at
+bs 32 (16384 tokens) through the HIP kernels (GEMM, FlashAttention, fused CE,
+AdamW), on synthetic uniform tokens and random-init weights.
+
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+
+Prints ONE JSON line. ``value`` = tokens/s over the timed steps (inputs and
+weights already resident in HBM). ``roofline`` = the dominant kernel's
+algorithmic work per launch / its mean duration, timed with HIP events on the
+stream it is launched on during the timed steps. ``cpu_baseline`` = the NumPy
+restatement of the same step (the oracle) on the host's cores, bs 4 sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from collections import defaultdict
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def _args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch-size", type=int, default=32)
+    ap.add_argument("--seq-len", type=int, default=512)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
+    return ap.parse_args()
+
+
+class KernelProbe:
+    """Brackets every libnlearn_hip call with HIP events on the current stream."""
+
+    def __init__(self, torch):
+        self.torch = torch
+        self.pending = []
+        self.enabled = False
+
+    @staticmethod
+    def tag(name, args):
+        if name in ("nl_gemm", "nl_gemm_ex"):
+            opA, opB, M, N, K = args[1:6]
+            return f"gemm_{'NT'[opA]}{'NT'[opB]}_{M}x{N}x{K}", 2.0 * M * N * K, "flops"
+        if name == "nl_ce_fwd_bwd":
+            M, V = args[1:3]
+            return f"ce_fwd_bwd_{M}x{V}", 4.0 * M * V + 12.0 * M, "bytes"
+        if name == "nl_flash_attention_fwd":
+            B, H, S, D = args[1:5]
+            f = 2.0 * B * H * S * S * D if args[6] else 4.0 * B * H * S * S * D
+            return f"flash_fwd_{B * H}x{S}x{D}", f, "flops"
+        if name == "nl_flash_attention_bwd":
+            B, H, S, D = args[1:5]
+            f = 2.0 * B * H * S * S * D if args[6] else 4.0 * B * H * S * S * D
+            return f"flash_bwd_{B * H}x{S}x{D}", 2.5 * f, "flops"
+        return None
+
+    def __call__(self, name, args):
+        if not self.enabled:
+            return None
+        t = self.tag(name, args)
+        if t is None:
+            return None
+        probe = self
+
+        class _Ctx:
+            def __enter__(self_inner):
+                self_inner.e0 = probe.torch.cuda.Event(enable_timing=True)
+                self_inner.e1 = probe.torch.cuda.Event(enable_timing=True)
+                self_inner.e0.record()
+
+            def __exit__(self_inner, *exc):
+                self_inner.e1.record()
+                probe.pending.append((t, self_inner.e0, self_inner.e1))
+                return False
+
+        return _Ctx()
+
+    def summary(self, steps):
+        agg = defaultdict(lambda: [0.0, 0, 0.0, ""])
+        for (tag, work, kind), e0, e1 in self.pending:
+            a = agg[tag]
+            a[0] += e0.elapsed_time(e1) * 1e-3
+            a[1] += 1
+            a[2] = work
+            a[3] = kind
+        out = {}
+        for tag, (tot, n, work, kind) in agg.items():
+            avg = tot / n
+            rate = work / avg
+            if kind == "flops":
+                out[tag] = {"bound": "mfma", "achieved": rate / 1e12, "peak": PEAK_BF16_TFLOPS,
+                            "unit": "TFLOP/s", "avg_us": avg * 1e6, "launches_per_step": n / steps,
+                            "time_per_step_ms": tot / steps * 1e3, "work_per_launch": work}
+            else:
+                out[tag] = {"bound": "hbm", "achieved": rate / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                            "avg_us": avg * 1e6, "launches_per_step": n / steps,
+                            "time_per_step_ms": tot / steps * 1e3, "work_per_launch": work}
+            out[tag]["frac"] = out[tag]["achieved"] / out[tag]["peak"]
+        return out
+
+
+def cpu_baseline(seconds: float):
+    """Time the NumPy restatement of the training step (bs 4, seq 512) on the host."""
+    import numpy as np
+
+    from oracle import model_np
+
+    cores = len(os.sched_getaffinity(0))
+    bs, seq = 4, 512
+    step = model_np.TrainStepNP(model_np.init_params(0), lr=3e-4)
+    rng = np.random.default_rng(0)
+    batch = rng.integers(0, 50257, (bs, seq + 1)).astype(np.int64)
+    t0 = time.time()
+    step(batch)  # warm-up (page-in, BLAS threads)
+    times = []
+    while True:
+        t1 = time.time()
+        step(batch)
+        times.append(time.time() - t1)
+        if time.time() - t0 > seconds or len(times) >= 5:
+            break
+    t = float(np.median(times))
+    return {"value": bs * seq / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"NumPy fp32 restatement of one train step (fwd+bwd+AdamW), bs {bs} x seq {seq}, "
+                      f"median of {len(times)} steps after 1 warm-up; {t:.2f} s/step"}
+
+
+def main():
+    a = _args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the data-parallel step would all-reduce "
+              "gradients over RCCL; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from nlearn_amd import _lib
+    from nlearn_amd.model import ModelConfig, flops_per_step, init_model
+    from nlearn_amd.train import AdamW, SyntheticTokens, make_train_step, warmup_cosine_decay_schedule
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    dev = torch.device("cuda:0")
+    bs, seq = a.batch_size, a.seq_len
+    cfg = ModelConfig(max_seq_len=max(512, seq))
+    params = init_model(0, cfg, dev)
+    total_updates = a.warmup + a.steps
+    opt = AdamW(warmup_cosine_decay_schedule(0.0, 1e-3, 200, max(total_updates, 1000), 1e-4))
+    state = opt.init(params)
+    step = make_train_step(opt, cfg)
+    data = SyntheticTokens(bs, seq, cfg.vocab_size, seed=0, device=dev)
+    batches = [data.get_batch() for _ in range(4)]
+
+    for i in range(a.warmup):
+        params, state, loss = step(params, state, batches[i % 4])
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+
+    probe = KernelProbe(torch)
+    _lib.set_probe(probe)
+    probe.enabled = True
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.steps):
+        params, state, loss = step(params, state, batches[i % 4])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    probe.enabled = False
+    _lib.set_probe(None)
+
+    tokens = bs * seq
+    ms = dt / a.steps * 1e3
+    value = tokens * a.steps / dt
+    kernels = probe.summary(a.steps)
+    dom_tag = max(kernels, key=lambda k: kernels[k]["time_per_step_ms"]) if kernels else None
+    roof = None
+    if dom_tag:
+        k = kernels[dom_tag]
+        roof = {"bound": k["bound"], "achieved": round(k["achieved"], 2), "peak": k["peak"], "unit": k["unit"],
+                "frac": round(k["frac"], 4), "traffic": None, "kernel": dom_tag, "avg_us": round(k["avg_us"], 2)}
+    fl = flops_per_step(cfg, bs, seq)
+    probed_ms = sum(k["time_per_step_ms"] for k in kernels.values())
+    out = {
+        "metric": "train tokens/sec d512/4L/seq512 bs32 (1 GPU)",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic uniform tokens, random-init weights (seeded)",
+        "config": {"workload": f"train_step fwd+bwd+AdamW d512/8h/4L vocab50257 bs{bs} seq{seq}",
+                   "global_batch": bs, "seq_len": seq, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "cpu_baseline": None,
+        "detail": {
+            "mfu_matmul": round(fl["total"] / (dt / a.steps) / (PEAK_BF16_TFLOPS * 1e12), 4),
+            "matmul_tflop_per_step": round(fl["total"] / 1e12, 4),
+            "six_n_t_tflops": round(fl["six_n_t"] / (dt / a.steps) / 1e12, 2),
+            "peak_hbm_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+            "nlearn_kernels_busy_ratio": round(probed_ms / ms, 4),
+            "final_loss": round(float(loss), 4),
+            "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                        for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["time_per_step_ms"])},
+        },
+    }
+    if not a.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
+        except ImportError as e:  # oracle absent from the tree
+            out["cpu_baseline"] = {"error": str(e)}
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -83,6 +83,19 @@ int nl_gemm(void* stream, int opA, int opB, int M, int N, int K,
             float beta, void* C, int c_dtype, int64_t ldc,
             const float* alpha_dev);
 
+/* nl_gemm with a caller-owned device workspace. Products with a small output
+ * and a long reduction (the weight gradient X^T.dY reduces over all tokens)
+ * split K across workgroups into fp32 partials that a second kernel sums in a
+ * fixed order (deterministic). nl_gemm_ws_bytes() gives the size this build
+ * wants for a shape (0 = no split); a NULL or smaller workspace just disables
+ * the split. Same result contract as nl_gemm. */
+size_t nl_gemm_ws_bytes(int opA, int opB, int M, int N, int K);
+int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K,
+               float alpha, const nl_bf16* A, int64_t lda,
+               const nl_bf16* B, int64_t ldb,
+               float beta, void* C, int c_dtype, int64_t ldc,
+               const float* alpha_dev, void* ws, size_t ws_bytes);
+
 /* ======================================================================== */
 /* Causal FlashAttention (head dim 64)                                        */
 /* ======================================================================== */
@@ -103,9 +116,10 @@ typedef struct nl_attn_stride {
 
 /*
  * O = softmax(scale * Q K^T + causal mask) V,  L = logsumexp row (natural log).
- * Requires d_head == 64, seq >= 1 (any length; tails masked), strides multiples
- * of 8 elements and 16-byte aligned bases. causal must be 1 (the reference path
- * is causal-only, flash_attention.metal:107).
+ * Requires d_head == 64, seq >= 0 (any length; tails masked), strides multiples
+ * of 8 elements with row >= 64, and 16-byte aligned bases. causal = 1 is the
+ * reference's causal mask (flash_attention.metal:107); causal = 0 attends to
+ * every key.
  * Replaces "flash_attention_fwd" (attention.py:82-91, flash_attention.metal:55-146).
  */
 int nl_flash_attention_fwd(void* stream, int batch, int heads, int seq, int d_head,
@@ -205,6 +219,24 @@ int nl_mean_f32(void* stream, const float* x, int n, float* out);
  * unit cotangent costs one tiny launch. Replaces g * dlogits (cross_entropy.py:65). */
 int nl_scale_bf16_by_device_scalar(void* stream, nl_bf16* x, int64_t rows, int64_t cols,
                                    int64_t ld, const float* g);
+
+/* ======================================================================== */
+/* AdamW (the optimizer of the training step)                                */
+/* ======================================================================== */
+/*
+ * One decoupled-weight-decay Adam update of a [rows][cols] fp32 tensor (p, g,
+ * m, v dense with row stride cols), following optax.adamw as called at
+ * nlearn/train.py:504-505:
+ *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
+ *   p = p - lr * ( (m / bc1) / (sqrt(v / bc2) + eps) + wd * p )
+ * with bc1 = 1 - b1^t, bc2 = 1 - b2^t for update number t (1-based).
+ * If p_bf16 != NULL the updated weight is also written there as bf16 (row
+ * stride ld_bf16): the compute copy the next forward reads, so no separate
+ * cast pass is needed (model.py:372-375 casts every parameter each step).
+ */
+int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const float* g, float* m, float* v,
+                  nl_bf16* p_bf16, int64_t ld_bf16, float lr, float b1, float b2, float eps, float wd,
+                  float bc1, float bc2);
 
 #ifdef __cplusplus
 }

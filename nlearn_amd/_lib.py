@@ -41,6 +41,8 @@ _SIGNATURES = {
     "nl_last_error": [],
     "nl_version": [],
     "nl_gemm": [_P, _I, _I, _I, _I, _I, _F, _P, _I64, _P, _I64, _F, _P, _I, _I64, _P],
+    "nl_gemm_ws_bytes": [_I, _I, _I, _I, _I],
+    "nl_gemm_ex": [_P, _I, _I, _I, _I, _I, _F, _P, _I64, _P, _I64, _F, _P, _I, _I64, _P, _P, ctypes.c_size_t],
     "nl_flash_attention_fwd": [_P, _I, _I, _I, _I, _F, _I, _P, _S, _P, _S, _P, _S, _P, _S, _P],
     "nl_flash_attention_bwd_preprocess": [_P, _I, _I, _I, _I, _P, _S, _P, _S, _P],
     "nl_flash_attention_bwd_dq": [_P, _I, _I, _I, _I, _F, _I, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _S],
@@ -54,12 +56,14 @@ _SIGNATURES = {
     "nl_ce_fwd_bwd": [_P, _I, _I, _P, _I64, _P, _P, _P, _F, _P, _I64],
     "nl_mean_f32": [_P, _P, _I, _P],
     "nl_scale_bf16_by_device_scalar": [_P, _P, _I64, _I64, _I64, _P],
+    "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F],
 }
 _RESTYPES = {
     "nl_strerror": ctypes.c_char_p,
     "nl_last_error": ctypes.c_char_p,
     "nl_version": ctypes.c_char_p,
     "nl_flash_attention_bwd_ws_bytes": ctypes.c_size_t,
+    "nl_gemm_ws_bytes": ctypes.c_size_t,
 }
 
 EXPORTED = tuple(_SIGNATURES)
@@ -89,10 +93,28 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+_probe = None
+
+
+def set_probe(probe) -> None:
+    """Install (or clear with None) a callable ``probe(name, args) -> ctx``.
+
+    When set, every entry point call runs inside the context manager the probe
+    returns (or unwrapped if it returns None); used by bench.py to bracket
+    kernels with HIP events on the stream they are launched on."""
+    global _probe
+    _probe = probe
+
+
 def call(name: str, *args) -> None:
     """Invoke an ``nl_*`` status-returning entry point; raise NlError on failure."""
     lib = load()
-    rc = getattr(lib, name)(*args)
+    ctx = _probe(name, args) if _probe is not None else None
+    if ctx is None:
+        rc = getattr(lib, name)(*args)
+    else:
+        with ctx:
+            rc = getattr(lib, name)(*args)
     if rc != NL_OK:
         msg = lib.nl_last_error().decode() or lib.nl_strerror(rc).decode()
         raise NlError(name, rc, msg)

@@ -346,8 +346,9 @@ extern "C" int nl_scale_bf16_by_device_scalar(void* stream, nl_bf16* x, int64_t 
   if (rows < 0 || cols < 0 || ld < cols || !g) return nl_set_error(NL_EINVAL, "scale: bad arguments");
   if (rows == 0 || cols == 0) return NL_OK;
   if (!x) return nl_set_error(NL_EINVAL, "scale: null x");
-  const int64_t gy = rows < 65535 ? rows : 65535;
-  const int64_t gx = (cols + 255) / 256 < 1024 ? (cols + 255) / 256 : 1024;
+  // a modest grid-stride launch: when *g == 1 every workgroup exits after one load
+  const int64_t gx = std::min<int64_t>((cols + 255) / 256, 8);
+  const int64_t gy = std::min<int64_t>(rows, 1024);
   hipLaunchKernelGGL(scale_rows_kernel, dim3((unsigned)gx, (unsigned)gy), dim3(256), 0, (hipStream_t)stream, x, rows,
                      cols, ld, g);
   return nl_check_launch("nl_scale_bf16_by_device_scalar");

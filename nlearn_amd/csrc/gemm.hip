@@ -40,6 +40,11 @@ struct GemmArgs {
   int64_t ldc;
   float alpha, beta;
   const float* alpha_dev;
+  // split-K: workgroup b handles tile b % tiles over k in [split*k_chunk, +k_chunk)
+  int tiles;
+  int k_chunk;
+  float* ws;      // fp32 partials [split][M][ldw] when splitting, else null
+  int64_t ldw;
 };
 
 __device__ __forceinline__ int swz(int row, int kc) { return (kc ^ ((row ^ (row >> 3)) & 7)); }
@@ -157,8 +162,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   const int wm = wave / WN, wn = wave % WN;
 
   const int tiles_n = (g.N + BN - 1) / BN;
-  const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+  const int split = blockIdx.x / g.tiles;
+  const int tile = blockIdx.x - split * g.tiles;
+  const int tm = tile / tiles_n, tn = tile % tiles_n;
   const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = split * g.k_chunk;
+  const int kend = min(g.K, kbeg + g.k_chunk);
 
   TileLoader<BM, NT, A_KMAJ> la;
   TileLoader<BN, NT, B_KMAJ> lb;
@@ -171,10 +180,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = (g.K + BK - 1) / BK;
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   if (nk > 0) {
-    la.load(g.A, g.lda, m0, g.M, 0, g.K, tid);
-    lb.load(g.B, g.ldb, n0, g.N, 0, g.K, tid);
+    la.load(g.A, g.lda, m0, g.M, kbeg, kend, tid);
+    lb.load(g.B, g.ldb, n0, g.N, kbeg, kend, tid);
     la.store(smem[0], tid);
     lb.store(smem[0] + BM * BK, tid);
     __syncthreads();
@@ -187,8 +196,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
     const int buf = kt & 1;
     const bool more = (kt + 1) < nk;
     if (more) {
-      la.load(g.A, g.lda, m0, g.M, (kt + 1) * BK, g.K, tid);
-      lb.load(g.B, g.ldb, n0, g.N, (kt + 1) * BK, g.K, tid);
+      la.load(g.A, g.lda, m0, g.M, kbeg + (kt + 1) * BK, kend, tid);
+      lb.load(g.B, g.ldb, n0, g.N, kbeg + (kt + 1) * BK, kend, tid);
     }
     const uint16_t* As = smem[buf];
     const uint16_t* Bs = smem[buf] + BM * BK;
@@ -218,11 +227,29 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
     __syncthreads();
   }
 
+  const int g4 = (lane >> 5) * 4;
+  if (g.ws) {  // split-K partial: raw fp32 sums, reduced by splitk_reduce_kernel
+    float* W = g.ws + (int64_t)split * g.M * g.ldw;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WTM + i * 32 + frow;
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
+          if (n < g.N)  // ldw is a multiple of 4 >= N: the 4-wide store stays in the row
+            *reinterpret_cast<f32x4*>(W + (int64_t)m * g.ldw + n) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
+    }
+    return;
+  }
   // epilogue: lane holds C[m][n..n+3] for m = row of lane, n = 8q + 4*(lane/32)
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
   OutT* C = reinterpret_cast<OutT*>(g.C);
-  const int g4 = (lane >> 5) * 4;
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm * WTM + i * 32 + frow;
@@ -261,29 +288,109 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 
 // beta*C for the degenerate K == 0 case is handled by the main kernel (nk = 0).
 
-template <int BM, int BN, int WM, int WN, bool AK, bool BK_, typename OutT>
-void launch_cfg(const GemmArgs& g, hipStream_t st) {
-  const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(tiles), dim3(WM * WN * 64), 0, st, g);
-}
-
-template <bool AK, bool BK_, typename OutT>
-void launch_layout(const GemmArgs& g, hipStream_t st) {
-  const int64_t big = (int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256);
-  if (big >= 512) {
-    launch_cfg<256, 256, 2, 2, AK, BK_, OutT>(g, st);
-  } else {
-    launch_cfg<128, 128, 2, 2, AK, BK_, OutT>(g, st);
+// C = alpha * s * sum_split ws[split] + beta * C, summed in split order (deterministic).
+template <typename OutT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int splits) {
+  const int64_t groups_n = (g.N + 3) / 4;
+  const int64_t total = (int64_t)g.M * groups_n;
+  float s = g.alpha;
+  if (g.alpha_dev) s *= *g.alpha_dev;
+  OutT* C = reinterpret_cast<OutT*>(g.C);
+  const int64_t plane = (int64_t)g.M * g.ldw;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / groups_n;
+    const int n = (int)(i - m * groups_n) * 4;
+    const float* w = g.ws + m * g.ldw + n;
+    f32x4 acc = *reinterpret_cast<const f32x4*>(w);
+    for (int sp = 1; sp < splits; ++sp) {
+      const f32x4 p = *reinterpret_cast<const f32x4*>(w + sp * plane);
+      acc[0] += p[0];
+      acc[1] += p[1];
+      acc[2] += p[2];
+      acc[3] += p[3];
+    }
+    OutT* crow = C + m * g.ldc;
+    if (n + 4 <= g.N) {
+      float v[4] = {acc[0] * s, acc[1] * s, acc[2] * s, acc[3] * s};
+      if (g.beta != 0.f)
+        for (int e = 0; e < 4; ++e) v[e] += g.beta * load1(crow + n + e);
+      store4(crow + n, v[0], v[1], v[2], v[3]);
+    } else {
+      for (int e = 0; e < 4 && n + e < g.N; ++e) {
+        float v = acc[e] * s;
+        if (g.beta != 0.f) v += g.beta * load1(crow + n + e);
+        store1(crow + n + e, v);
+      }
+    }
   }
 }
 
+// Tile configuration and K split of one product (shared by the workspace query).
+struct Plan {
+  int big;     // 1: 256x256 tiles, 0: 128x128
+  int tiles;
+  int splits;
+  int k_chunk;
+  int64_t ldw;
+  size_t ws_bytes;
+};
+
+Plan make_plan(int M, int N, int K) {
+  Plan p;
+  const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+  p.big = t256 >= 512;
+  const int bm = p.big ? 256 : 128;
+  p.tiles = (int)((int64_t)((M + bm - 1) / bm) * ((N + bm - 1) / bm));
+  p.splits = 1;
+  p.k_chunk = K > 0 ? K : 1;
+  // skinny outputs with a long reduction (weight gradients, K = tokens): split K
+  // until ~640 workgroups are in flight, keeping >= 512 k per split
+  if (p.tiles < 256 && K >= 1024) {
+    int want = (640 + p.tiles - 1) / p.tiles;
+    int maxs = K / 512;
+    int sp = want < maxs ? want : maxs;
+    if (sp > 1) {
+      int chunk = (K + sp - 1) / sp;
+      chunk = (chunk + BK - 1) / BK * BK;
+      p.k_chunk = chunk;
+      p.splits = (K + chunk - 1) / chunk;
+    }
+  }
+  p.ldw = ((int64_t)N + 7) / 8 * 8;
+  p.ws_bytes = p.splits > 1 ? (size_t)p.splits * M * p.ldw * sizeof(float) : 0;
+  return p;
+}
+
+template <int BM, int BN, int WM, int WN, bool AK, bool BK_, typename OutT>
+void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
+  g.tiles = p.tiles;
+  g.k_chunk = p.k_chunk;
+  if (p.splits > 1) {
+    g.ldw = p.ldw;  // g.ws already set by the caller
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles * p.splits), dim3(WM * WN * 64),
+                       0, st, g);
+    const int64_t work = (int64_t)g.M * ((g.N + 3) / 4);
+    const int blocks = (int)std::min<int64_t>((work + 255) / 256, 4096);
+    hipLaunchKernelGGL((splitk_reduce_kernel<OutT>), dim3(blocks), dim3(256), 0, st, g, p.splits);
+  } else {
+    g.ws = nullptr;
+    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles), dim3(WM * WN * 64), 0, st, g);
+  }
+}
+
+template <bool AK, bool BK_, typename OutT>
+void launch_layout(const GemmArgs& g, const Plan& p, hipStream_t st) {
+  if (p.big) launch_cfg<256, 256, 2, 2, AK, BK_, OutT>(g, p, st);
+  else launch_cfg<128, 128, 2, 2, AK, BK_, OutT>(g, p, st);
+}
+
 template <typename OutT>
-void launch_typed(int opA, int opB, const GemmArgs& g, hipStream_t st) {
+void launch_typed(int opA, int opB, const GemmArgs& g, const Plan& p, hipStream_t st) {
   // A is k-major when not transposed; B is k-major when transposed.
-  if (opA == NL_OP_N && opB == NL_OP_N) launch_layout<true, false, OutT>(g, st);
-  else if (opA == NL_OP_N && opB == NL_OP_T) launch_layout<true, true, OutT>(g, st);
-  else if (opA == NL_OP_T && opB == NL_OP_N) launch_layout<false, false, OutT>(g, st);
-  else launch_layout<false, true, OutT>(g, st);
+  if (opA == NL_OP_N && opB == NL_OP_N) launch_layout<true, false, OutT>(g, p, st);
+  else if (opA == NL_OP_N && opB == NL_OP_T) launch_layout<true, true, OutT>(g, p, st);
+  else if (opA == NL_OP_T && opB == NL_OP_N) launch_layout<false, false, OutT>(g, p, st);
+  else launch_layout<false, true, OutT>(g, p, st);
 }
 
 }  // namespace
@@ -291,9 +398,16 @@ void launch_typed(int opA, int opB, const GemmArgs& g, hipStream_t st) {
 
 using namespace nl;
 
-extern "C" int nl_gemm(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
-                       int64_t lda, const nl_bf16* B, int64_t ldb, float beta, void* C, int c_dtype, int64_t ldc,
-                       const float* alpha_dev) {
+extern "C" size_t nl_gemm_ws_bytes(int opA, int opB, int M, int N, int K) {
+  (void)opA;
+  (void)opB;
+  if (M <= 0 || N <= 0 || K <= 0) return 0;
+  return make_plan(M, N, K).ws_bytes;
+}
+
+extern "C" int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
+                          int64_t lda, const nl_bf16* B, int64_t ldb, float beta, void* C, int c_dtype, int64_t ldc,
+                          const float* alpha_dev, void* ws, size_t ws_bytes) {
   if (opA != NL_OP_N && opA != NL_OP_T) return nl_set_error(NL_EINVAL, "gemm: opA must be NL_OP_N or NL_OP_T");
   if (opB != NL_OP_N && opB != NL_OP_T) return nl_set_error(NL_EINVAL, "gemm: opB must be NL_OP_N or NL_OP_T");
   if (c_dtype != NL_DTYPE_F32 && c_dtype != NL_DTYPE_BF16) return nl_set_error(NL_EINVAL, "gemm: bad c_dtype");
@@ -323,8 +437,22 @@ extern "C" int nl_gemm(void* stream, int opA, int opB, int M, int N, int K, floa
   g.alpha = alpha;
   g.beta = beta;
   g.alpha_dev = alpha_dev;
+  Plan p = make_plan(M, N, K);
+  if (p.splits > 1 && (!ws || ws_bytes < p.ws_bytes || ((uintptr_t)ws & 15) != 0)) {
+    // no (usable) workspace: one workgroup per tile over the whole K range
+    p.splits = 1;
+    p.k_chunk = K > 0 ? K : 1;
+    p.ws_bytes = 0;
+  }
+  g.ws = static_cast<float*>(ws);
   hipStream_t st = (hipStream_t)stream;
-  if (c_dtype == NL_DTYPE_F32) launch_typed<float>(opA, opB, g, st);
-  else launch_typed<uint16_t>(opA, opB, g, st);
+  if (c_dtype == NL_DTYPE_F32) launch_typed<float>(opA, opB, g, p, st);
+  else launch_typed<uint16_t>(opA, opB, g, p, st);
   return nl_check_launch("nl_gemm");
+}
+
+extern "C" int nl_gemm(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
+                       int64_t lda, const nl_bf16* B, int64_t ldb, float beta, void* C, int c_dtype, int64_t ldc,
+                       const float* alpha_dev) {
+  return nl_gemm_ex(stream, opA, opB, M, N, K, alpha, A, lda, B, ldb, beta, C, c_dtype, ldc, alpha_dev, nullptr, 0);
 }

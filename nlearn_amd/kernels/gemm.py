@@ -94,11 +94,15 @@ def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", o
     if alpha_dev is not None and (alpha_dev.dtype != _F32 or not alpha_dev.is_cuda):
         raise ValueError("gemm: alpha_dev must be a float32 device scalar")
     stream = torch.cuda.current_stream(A.device).cuda_stream
-    _lib.call("nl_gemm", stream, _lib.NL_OP_T if opA == "T" else _lib.NL_OP_N,
-              _lib.NL_OP_T if opB == "T" else _lib.NL_OP_N, M, N, K, float(alpha),
+    oa = _lib.NL_OP_T if opA == "T" else _lib.NL_OP_N
+    ob = _lib.NL_OP_T if opB == "T" else _lib.NL_OP_N
+    wsb = int(_lib.load().nl_gemm_ws_bytes(oa, ob, M, N, K))
+    ws = torch.empty(wsb // 4, dtype=_F32, device=A.device) if wsb else None
+    _lib.call("nl_gemm_ex", stream, oa, ob, M, N, K, float(alpha),
               A.data_ptr(), _ld(A), B.data_ptr(), _ld(B), float(beta), out.data_ptr(),
               _lib.NL_DTYPE_F32 if out.dtype == _F32 else _lib.NL_DTYPE_BF16, _ld(out),
-              alpha_dev.data_ptr() if alpha_dev is not None else None)
+              alpha_dev.data_ptr() if alpha_dev is not None else None,
+              ws.data_ptr() if ws is not None else None, wsb)
     return out
 
 

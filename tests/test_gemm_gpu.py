@@ -128,3 +128,32 @@ def test_linear_autograd(dev):
     assert rel_l2(_np(xb.grad).reshape(-1, 64), ops.gemm(gn, Wn, "N", "T")) <= 5e-3
     assert Wp.grad.dtype == torch.float32
     assert rel_l2(Wp.grad.cpu().numpy(), ops.gemm(xn, gn, "T", "N")) <= 5e-3
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 512, 16384), (2048, 512, 16384), (512, 1536, 4096), (100, 70, 5000)])
+def test_gemm_split_k_matches_single_pass_and_is_deterministic(dev, M, N, K):
+    """Weight-gradient shapes (small output, long reduction) take the split-K
+    path when a workspace is given; it must agree with the one-pass kernel and
+    give bitwise-identical results run to run."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
+
+    gen = torch.Generator(device=dev).manual_seed(M + N + K)
+    X = padded_empty(K, M, torch.bfloat16, dev)   # A stored [K][M] (opA = T)
+    X.copy_(torch.randn((K, M), generator=gen, device=dev))
+    dY = padded_empty(K, N, torch.bfloat16, dev)
+    dY.copy_(torch.randn((K, N), generator=gen, device=dev))
+    assert _lib.load().nl_gemm_ws_bytes(1, 0, M, N, K) > 0
+    split1 = gemm_raw(X, dY, "T", "N", out_dtype=torch.float32)
+    split2 = gemm_raw(X, dY, "T", "N", out_dtype=torch.float32)
+    single = padded_empty(M, N, torch.float32, dev)
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.call("nl_gemm", st, 1, 0, M, N, K, 1.0, X.data_ptr(), X.stride(0), dY.data_ptr(), dY.stride(0), 0.0,
+              single.data_ptr(), 0, single.stride(0), None)
+    torch.cuda.synchronize()
+    assert torch.equal(split1, split2)
+    assert rel_l2(_np(split1), _np(single)) <= 1e-5
+    cols = np.random.default_rng(1).choice(N, min(N, 32), replace=False)
+    ct = torch.from_numpy(cols).to(dev)
+    assert rel_l2(_np(split1[:, ct]), ops.gemm(_np(X), _np(dY[:, ct]), "T", "N")) <= 5e-3
