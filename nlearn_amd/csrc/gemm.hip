@@ -6,22 +6,31 @@
 // accumulate, forward A.B, backward dA = dC.B^T and dB = A^T.dC) and
 // iree_metal/kernels/gemm.metal:48-115 (f32 accumulator per output).
 //
-// MI355X design
-//   * v_mfma_f32_32x32x16_bf16: each wave owns a (BM/WM) x (BN/WN) sub-tile
-//     held as FM x FN fp32 32x32 accumulators (AGPR-resident).
-//   * Both operands are staged in LDS as [row][k] with k contiguous, 64 k per
-//     stage, in a 16-byte-chunk XOR swizzle: chunk kc of row R lives at slot
-//     kc ^ ((R ^ R>>3) & 7). Fragment reads (8 consecutive rows, same chunk),
-//     row-contiguous writes and transposed writes are all conflict-free.
-//   * An operand whose contraction dim is strided in memory (B of the forward
-//     x.W, both operands of the weight gradient X^T.dY) is read as 8x8 bf16
-//     blocks with 16-byte loads and transposed in registers (v_perm_b32) before
-//     its LDS store, so no transposed copy is ever written to HBM.
-//   * Register-prefetch + LDS double buffer: the next stage's global loads are
-//     in flight while the MFMAs consume the current stage; one barrier/stage.
-//   * MFMA operands are swapped (B fragment as src A) so every lane ends up
-//     with 4 consecutive output columns: 16-byte fp32 / 8-byte bf16 stores.
-//   * M, N and K tails are masked in-kernel (zero-filled loads, guarded stores).
+// MI355X design (main path, gemm2_kernel)
+//   * 128 x 128 output tile per workgroup of 4 waves (2 x 2), each wave a 64 x 64
+//     block of fp32 32x32 MFMA accumulators (v_mfma_f32_32x32x16_bf16).
+//   * Operand tiles go global -> LDS with buffer_load_dwordx4 ... lds (LDS DMA):
+//     no staging registers and no ds_write; per-lane offsets are fixed for the
+//     whole K loop and the K advance is a scalar offset. The buffer range check
+//     clips rows past the matrix (no edge branches in the loop).
+//   * An operand whose contraction dim is contiguous is stored [row][k] in LDS
+//     with a 16-byte-chunk XOR swizzle and read with ds_read_b128; an operand
+//     whose contraction dim is strided (B of the forward x.W, both operands of
+//     the weight gradient X^T.dY) stays [k][row] as in memory and is read with
+//     ds_read_b64_tr_b16, the gfx950 transposing LDS read. Nothing is ever
+//     transposed in HBM or in registers.
+//   * Double-buffered LDS stages of 64 k (both operands k-major) or 32 k
+//     (otherwise: 32 KB per workgroup, more workgroups per CU to cover L2-miss
+//     latency), one barrier per stage.
+//   * Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of
+//     tiles in groups of 8 M-tiles, sharing A and B panels in its L2.
+//   * Small outputs with a long reduction (weight gradients) split K across
+//     workgroups into fp32 partials reduced in a fixed order (deterministic).
+//   * MFMA operands are swapped (B fragment as src A) so every lane ends up with
+//     4 consecutive output columns: 16-byte fp32 / 8-byte bf16 stores.
+//   * A ragged K tail is staged through registers with element masks.
+// The first-generation register-staged kernel (gemm_kernel) remains as the
+// path for operands beyond the 2 GB reach of 32-bit buffer offsets.
 #include "common.h"
 
 namespace nl {
@@ -101,6 +110,25 @@ struct TileLoader {
     }
   }
 
+  // Interior tile, full k stage: no bounds checks at all.
+  __device__ __forceinline__ void load_fast(const uint16_t* __restrict__ P, int64_t ld, int row0, int k0, int tid) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int u = i * NT + tid;
+      if (UNITS % NT == 0 || u < UNITS) {
+        if constexpr (KMAJ) {
+          const int row = u / CHUNKS, kc = u % CHUNKS;
+          r[i] = *reinterpret_cast<const u32x4*>(P + (int64_t)(row0 + row) * ld + k0 + kc * 8);
+        } else {
+          const int kb = u / (ROWS / 8), rb = u % (ROWS / 8);
+          const uint16_t* base = P + (int64_t)(k0 + kb * 8) * ld + row0 + rb * 8;
+#pragma unroll
+          for (int q = 0; q < 8; ++q) r[i * 8 + q] = *reinterpret_cast<const u32x4*>(base + (int64_t)q * ld);
+        }
+      }
+    }
+  }
+
   __device__ __forceinline__ void store(uint16_t* __restrict__ S, int tid) {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
@@ -161,13 +189,28 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   const int wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
+  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
+  // L2): give every XCD a contiguous run of logical ids, then walk tiles in
+  // groups of 8 M-tiles so the ~32 tiles an XCD runs at once share A and B panels.
+  int bid = blockIdx.x;
+  {
+    const int nwg = gridDim.x, per = nwg / 8;
+    if (bid < per * 8) bid = (bid % 8) * per + bid / 8;
+  }
   const int tiles_n = (g.N + BN - 1) / BN;
-  const int split = blockIdx.x / g.tiles;
-  const int tile = blockIdx.x - split * g.tiles;
-  const int tm = tile / tiles_n, tn = tile % tiles_n;
+  const int tiles_m = (g.M + BM - 1) / BM;
+  const int split = bid / g.tiles;
+  const int tile = bid - split * g.tiles;
+  constexpr int GM = 8;
+  const int in_group = GM * tiles_n;
+  const int first_m = (tile / in_group) * GM;
+  const int gsize = min(tiles_m - first_m, GM);
+  const int tm = first_m + (tile % in_group) % gsize;
+  const int tn = (tile % in_group) / gsize;
   const int m0 = tm * BM, n0 = tn * BN;
   const int kbeg = split * g.k_chunk;
   const int kend = min(g.K, kbeg + g.k_chunk);
+  const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
 
   TileLoader<BM, NT, A_KMAJ> la;
   TileLoader<BN, NT, B_KMAJ> lb;
@@ -180,51 +223,80 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  if (nk > 0) {
-    la.load(g.A, g.lda, m0, g.M, kbeg, kend, tid);
-    lb.load(g.B, g.ldb, n0, g.N, kbeg, kend, tid);
-    la.store(smem[0], tid);
-    lb.store(smem[0] + BM * BK, tid);
-    __syncthreads();
-  }
+  auto load_stage = [&](int k0) {
+    if (full_mn && k0 + BK <= kend) {
+      la.load_fast(g.A, g.lda, m0, k0, tid);
+      lb.load_fast(g.B, g.ldb, n0, k0, tid);
+    } else {
+      la.load(g.A, g.lda, m0, g.M, k0, kend, tid);
+      lb.load(g.B, g.ldb, n0, g.N, k0, kend, tid);
+    }
+  };
 
   const int frow = lane & 31;   // row within a 32-row fragment
   const int fkc = lane >> 5;    // which 8-k half of a 16-k step
+  // per-lane LDS row offsets (elements) and swizzle keys of the fragment rows
+  int aoff[FM], asw[FM], boff[FN], bsw[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int row = wm * WTM + i * 32 + frow;
+    aoff[i] = row * BK;
+    asw[i] = (row ^ (row >> 3)) & 7;
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int row = wn * WTN + j * 32 + frow;
+    boff[j] = BM * BK + row * BK;
+    bsw[j] = (row ^ (row >> 3)) & 7;
+  }
+  bf16x8 af[2][FM], bfr[2][FN];
+  auto load_frags = [&](const uint16_t* sb, int ks, int slot) {
+    const int kc = ks * 2 + fkc;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[slot][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + aoff[i] + ((kc ^ asw[i]) << 3)));
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      bfr[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + boff[j] + ((kc ^ bsw[j]) << 3)));
+  };
+
+  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+  if (nk > 0) {
+    load_stage(kbeg);
+    la.store(smem[0], tid);
+    lb.store(smem[0] + BM * BK, tid);
+    __syncthreads();
+    load_frags(smem[0], 0, 0);
+  }
 
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     const bool more = (kt + 1) < nk;
-    if (more) {
-      la.load(g.A, g.lda, m0, g.M, kbeg + (kt + 1) * BK, kend, tid);
-      lb.load(g.B, g.ldb, n0, g.N, kbeg + (kt + 1) * BK, kend, tid);
-    }
-    const uint16_t* As = smem[buf];
-    const uint16_t* Bs = smem[buf] + BM * BK;
+    if (more) load_stage(kbeg + (kt + 1) * BK);
+    const uint16_t* sb = smem[buf];
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      const int kc = ks * 2 + fkc;
-      bf16x8 af[FM], bfr[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int row = wm * WTM + i * 32 + frow;
-        af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(As + row * BK + swz(row, kc) * 8));
-      }
-#pragma unroll
-      for (int j = 0; j < FN; ++j) {
-        const int row = wn * WTN + j * 32 + frow;
-        bfr[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(Bs + row * BK + swz(row, kc) * 8));
-      }
+      const int cur = ks & 1;
+      if (ks + 1 < BK / 16) load_frags(sb, ks + 1, cur ^ 1);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[j], af[i], acc[i][j]);
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[cur][j], af[cur][i], acc[i][j]);
+      if (ks + 1 < BK / 16) {
+        // interleave the next sub-step's fragment reads with this sub-step's MFMAs
+#pragma unroll
+        for (int x = 0; x < FM + FN; ++x) {
+          __builtin_amdgcn_sched_group_barrier(0x008, (FM * FN) / (FM + FN) > 0 ? (FM * FN) / (FM + FN) : 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+      }
     }
     if (more) {
       la.store(smem[buf ^ 1], tid);
       lb.store(smem[buf ^ 1] + BM * BK, tid);
     }
     __syncthreads();
+    if (more) load_frags(smem[buf ^ 1], 0, 0);
   }
 
   const int g4 = (lane >> 5) * 4;
@@ -286,6 +358,342 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   }
 }
 
+// ===========================================================================
+// v2 main loop: LDS DMA + transposing LDS reads
+//
+//   * Global -> LDS with buffer_load_dwordx4 ... lds: no staging registers, no
+//     ds_write. Per-lane byte offsets are fixed for the whole K loop; the K
+//     advance is a scalar soffset. The buffer's num_records clips rows past
+//     the matrix (they read as zero, so no edge branches).
+//   * K-major tile (rows x 64 k): [row][k] with the 16-byte-chunk XOR swizzle
+//     of the v1 kernel; MFMA fragments are single ds_read_b128.
+//   * MN-major tile (64 k x rows): stored as it sits in memory, [k][row], with
+//     chunk c of k-row k at slot c ^ (2k & 15); an MFMA fragment (8 k of one
+//     row) is two ds_read_b64_tr_b16, which deliver 4 consecutive k of a column
+//     to each lane of a 16-lane group. No register transposes at all.
+//   * A ragged K tail (K % 64 != 0) is staged once through registers with
+//     element masks into the same layouts.
+// ===========================================================================
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kNW = 4;  // waves per workgroup (2 x 2)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// K-major tiles keep CH = BKT/8 16-byte chunks per row; chunk kc of row r sits
+// at slot kc ^ kswz(r). Eight consecutive rows at one chunk (a fragment read)
+// land on distinct banks for CH = 8 and CH = 4.
+template <int CH>
+__device__ __forceinline__ int kswz(int r) {
+  if constexpr (CH == 8) return (r ^ (r >> 3)) & 7;
+  else return (r >> 1) & 3;
+}
+
+// Per-lane DMA offsets of one ROWS x BKT operand tile.
+template <int ROWS, int BKT, bool KMAJ>
+struct Dma {
+  static constexpr int CH = BKT / 8;
+  static constexpr int INSTR = ROWS * BKT / 8 / 64 / kNW;  // per wave per stage
+  uint32_t voff[INSTR];  // bytes from the operand base for k0 = 0
+  __device__ __forceinline__ void init(int row0, int64_t ld, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      if constexpr (KMAJ) {
+        const int r = (i * kNW + wave) * (64 / CH) + lane / CH;
+        const int kc = (lane % CH) ^ kswz<CH>(r);
+        voff[i] = (uint32_t)(((int64_t)(row0 + r) * ld + kc * 8) * 2);
+      } else {
+        constexpr int CPR = ROWS / 8, RPI = 64 / CPR;
+        const int k = (i * kNW + wave) * RPI + lane / CPR;
+        const int c = (lane % CPR) ^ ((2 * k) & 15);
+        voff[i] = (uint32_t)(((int64_t)k * ld + row0 + c * 8) * 2);
+      }
+    }
+  }
+  // issue the stage whose first k is k0 into the tile at `lds`
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, uint16_t* lds, int k0, int64_t ld, int wave) {
+    const uint32_t soff = KMAJ ? (uint32_t)(k0 * 2) : (uint32_t)((int64_t)k0 * ld * 2);
+#pragma unroll
+    for (int i = 0; i < INSTR; ++i) {
+      const int base_elems = (i * kNW + wave) * 512;  // each instruction fills 64 x 16 bytes
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds + base_elems), 16, voff[i], soff, 0, 0);
+    }
+  }
+};
+
+// Masked register staging of one stage (used for a ragged K tail only).
+template <int ROWS, int BKT, bool KMAJ, int NT>
+__device__ __forceinline__ void stage_masked(const uint16_t* __restrict__ P, int64_t ld, int row0, int rows_lim,
+                                             int k0, int k_lim, uint16_t* lds, int tid) {
+  constexpr int CH = BKT / 8;
+  constexpr int UNITS = ROWS * CH;  // 16-byte chunks
+#pragma unroll
+  for (int i = 0; i < (UNITS + NT - 1) / NT; ++i) {
+    const int u = i * NT + tid;
+    if (u >= UNITS) break;
+    if constexpr (KMAJ) {
+      const int r = u / CH, kc = u % CH;
+      const int grow = row0 + r, gk = k0 + kc * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (grow < rows_lim) v = load8(P + (int64_t)grow * ld + gk, k_lim - gk);
+      *reinterpret_cast<u32x4*>(lds + r * BKT + ((kc ^ kswz<CH>(r)) << 3)) = v;
+    } else {
+      constexpr int CPR = ROWS / 8;
+      const int k = u / CPR, c = u % CPR;
+      const int gk = k0 + k, gm = row0 + c * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (gk < k_lim) v = load8(P + (int64_t)gk * ld + gm, rows_lim - gm);
+      *reinterpret_cast<u32x4*>(lds + k * ROWS + ((c ^ ((2 * k) & 15)) << 3)) = v;
+    }
+  }
+}
+
+// Fragment reader for a 32-row block of a tile: 8 bf16 of k = ks*16 + 8g .. +7.
+template <int ROWS, int BKT, bool KMAJ>
+struct Frag {
+  static constexpr int CH = BKT / 8;
+  int off[2];   // per-lane element offsets (K-major: row start; MN-major: two tr reads)
+  int sw;       // K-major: row swizzle key
+  __device__ __forceinline__ void init(int row, int lane) {
+    if constexpr (KMAJ) {
+      const int r = row + (lane & 31);
+      off[0] = r * BKT;
+      sw = kswz<CH>(r);
+    } else {
+      const int G = lane >> 4, j = lane & 15;
+      const int g = G >> 1, h = G & 1;
+      const int mn = row + 16 * h + 4 * (j & 3);
+#pragma unroll
+      for (int rr = 0; rr < 2; ++rr) {
+        const int k = 8 * g + 4 * rr + (j >> 2);  // + ks*16 (does not change the swizzle key)
+        off[rr] = k * ROWS + (((mn >> 3) ^ ((2 * k) & 15)) << 3) + (mn & 7);
+      }
+      sw = 0;
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const uint16_t* tile, int ks, int lane) const {
+    if constexpr (KMAJ) {
+      const int kc = ks * 2 + (lane >> 5);
+      return as_bf16x8(*reinterpret_cast<const u32x4*>(tile + off[0] + ((kc ^ sw) << 3)));
+    } else {
+      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+      const uint16_t* t = tile + ks * 16 * ROWS;
+      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off[0]));
+      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off[1]));
+      u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+      return as_bf16x8(u32x4{a[0], a[1], b[0], b[1]});
+    }
+  }
+};
+
+// s_waitcnt vmcnt(n) (other counters unconstrained), n < 64
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// wait until at most `later` stages (IPS DMA ops each) of this wave are outstanding
+template <int IPS, int MAXL>
+__device__ __forceinline__ void wait_stage(int later) {
+  if constexpr (MAXL <= 0) {
+    wait_vm<0>();
+  } else {
+    if (later >= MAXL) wait_vm<MAXL * IPS>();
+    else wait_stage<IPS, MAXL - 1>(later);
+  }
+}
+
+template <int BM, int BN, int BKT, int S, bool A_KMAJ, bool B_KMAJ, typename OutT>
+__global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
+  constexpr int NT = 256;
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int FM = WTM / 32, FN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * BKT;  // elements per stage
+  __shared__ __attribute__((aligned(16))) uint16_t smem[S * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+
+  int bid = blockIdx.x;
+  {
+    const int nwg = gridDim.x, per = nwg / 8;
+    if (bid < per * 8) bid = (bid % 8) * per + bid / 8;
+  }
+  const int tiles_n = (g.N + BN - 1) / BN;
+  const int tiles_m = (g.M + BM - 1) / BM;
+  const int split = bid / g.tiles;
+  const int tile = bid - split * g.tiles;
+  constexpr int GM = 8;
+  const int in_group = GM * tiles_n;
+  const int first_m = (tile / in_group) * GM;
+  const int gsize = min(tiles_m - first_m, GM);
+  const int tm = first_m + (tile % in_group) % gsize;
+  const int tn = (tile % in_group) / gsize;
+  const int m0 = tm * BM, n0 = tn * BN;
+  const int kbeg = split * g.k_chunk;
+  const int kend = min(g.K, kbeg + g.k_chunk);
+  const int nfull = kend > kbeg ? (kend - kbeg) / BKT : 0;
+  const bool tail = kend > kbeg && ((kend - kbeg) % BKT) != 0;
+
+  // Buffer descriptors clip at the end of each logical matrix, rounded up to
+  // the 16-byte chunk that holds its last element: the range check zeroes
+  // whole dwords, and an aligned chunk never crosses a page. The extra columns
+  // only reach outputs that are not stored; a ragged K tail is staged with
+  // element masks instead.
+  const uint32_t a_bytes = (uint32_t)((((A_KMAJ ? (int64_t)(g.M - 1) * g.lda + g.K
+                                                : (int64_t)(g.K - 1) * g.lda + g.M) * 2) + 15) & ~(int64_t)15);
+  const uint32_t b_bytes = (uint32_t)((((B_KMAJ ? (int64_t)(g.N - 1) * g.ldb + g.K
+                                                : (int64_t)(g.K - 1) * g.ldb + g.N) * 2) + 15) & ~(int64_t)15);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, b_bytes);
+  Dma<BM, BKT, A_KMAJ> da;
+  Dma<BN, BKT, B_KMAJ> db;
+  da.init(m0, g.lda, wave, lane);
+  db.init(n0, g.ldb, wave, lane);
+  constexpr int IPS = Dma<BM, BKT, A_KMAJ>::INSTR + Dma<BN, BKT, B_KMAJ>::INSTR;  // DMA ops per stage per wave
+
+  Frag<BM, BKT, A_KMAJ> fa[FM];
+  Frag<BN, BKT, B_KMAJ> fb[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[i].init(wm * WTM + i * 32, lane);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[j].init(wn * WTN + j * 32, lane);
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  bf16x8 af[2][FM], bfr[2][FN];
+  auto compute = [&](const uint16_t* sb) {
+    const uint16_t* As = sb;
+    const uint16_t* Bs = sb + BM * BKT;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = fa[i].read(As, 0, lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bfr[0][j] = fb[j].read(Bs, 0, lane);
+#pragma unroll
+    for (int ks = 0; ks < BKT / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < BKT / 16) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[cur ^ 1][i] = fa[i].read(As, ks + 1, lane);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[cur ^ 1][j] = fb[j].read(Bs, ks + 1, lane);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[cur][j], af[cur][i], acc[i][j]);
+    }
+  };
+  auto issue = [&](int st) {  // DMA of full stage st (0-based within this split)
+    uint16_t* sb = smem + (st % S) * STAGE;
+    const int k0 = kbeg + st * BKT;
+    da.issue(ra, sb, k0, g.lda, wave);
+    db.issue(rb, sb + BM * BKT, k0, g.ldb, wave);
+  };
+
+  // prologue: S-1 stages in flight
+#pragma unroll
+  for (int st = 0; st < S - 1; ++st)
+    if (st < nfull) issue(st);
+  for (int kt = 0; kt < nfull; ++kt) {
+    // stage kt has landed once at most min(S-2, nfull-1-kt) later stages are outstanding
+    wait_stage<IPS, S - 2>(min(S - 2, nfull - 1 - kt));
+    __syncthreads();  // stage kt visible to all waves; all waves are done with stage kt-1
+    if (kt + S - 1 < nfull) issue(kt + S - 1);
+    compute(smem + (kt % S) * STAGE);
+  }
+  if (tail) {
+    __syncthreads();
+    uint16_t* sb = smem + (nfull % S) * STAGE;
+    const int kt0 = kbeg + nfull * BKT;
+    stage_masked<BM, BKT, A_KMAJ, NT>(g.A, g.lda, m0, g.M, kt0, kend, sb, tid);
+    stage_masked<BN, BKT, B_KMAJ, NT>(g.B, g.ldb, n0, g.N, kt0, kend, sb + BM * BKT, tid);
+    __syncthreads();
+    compute(sb);
+  }
+  const int frow = lane & 31;
+  const int g4 = (lane >> 5) * 4;
+  if (g.ws) {
+    float* W = g.ws + (int64_t)split * g.M * g.ldw;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WTM + i * 32 + frow;
+      if (m >= g.M) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
+          if (n < g.N)
+            *reinterpret_cast<f32x4*>(W + (int64_t)m * g.ldw + n) =
+                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        }
+    }
+    return;
+  }
+  float s = g.alpha;
+  if (g.alpha_dev) s *= *g.alpha_dev;
+  OutT* C = reinterpret_cast<OutT*>(g.C);
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int m = m0 + wm * WTM + i * 32 + frow;
+    if (m >= g.M) continue;
+    OutT* crow = C + (int64_t)m * g.ldc;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
+        float v0 = acc[i][j][4 * q + 0] * s, v1 = acc[i][j][4 * q + 1] * s;
+        float v2 = acc[i][j][4 * q + 2] * s, v3 = acc[i][j][4 * q + 3] * s;
+        if (n + 4 <= g.N) {
+          if (g.beta != 0.f) {
+            v0 += g.beta * load1(crow + n + 0);
+            v1 += g.beta * load1(crow + n + 1);
+            v2 += g.beta * load1(crow + n + 2);
+            v3 += g.beta * load1(crow + n + 3);
+          }
+          store4(crow + n, v0, v1, v2, v3);
+        } else {
+          const float vv[4] = {v0, v1, v2, v3};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (n + e < g.N) {
+              float v = vv[e];
+              if (g.beta != 0.f) v += g.beta * load1(crow + n + e);
+              store1(crow + n + e, v);
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Explicit instantiations: every (tile, pipeline, layout, output) combination
+// the dispatcher can launch gets its host stub emitted.
+#define NL_I(BM, BKT, S, AK, BKM, T) template __global__ void gemm2_kernel<BM, BM, BKT, S, AK, BKM, T>(GemmArgs);
+#define NL_I4(BM, BKT, S, T)                                                                 \
+  NL_I(BM, BKT, S, true, false, T) NL_I(BM, BKT, S, true, true, T) NL_I(BM, BKT, S, false, false, T) \
+  NL_I(BM, BKT, S, false, true, T)
+#define NL_I8(BM, BKT, S) NL_I4(BM, BKT, S, float) NL_I4(BM, BKT, S, uint16_t)
+NL_I8(128, 64, 2)
+NL_I8(128, 32, 2)
+#undef NL_I8
+#undef NL_I4
+#undef NL_I
+
 // beta*C for the degenerate K == 0 case is handled by the main kernel (nk = 0).
 
 // C = alpha * s * sum_split ws[split] + beta * C, summed in split order (deterministic).
@@ -338,7 +746,10 @@ struct Plan {
 Plan make_plan(int M, int N, int K) {
   Plan p;
   const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  p.big = t256 >= 512;
+  (void)t256;
+  // 128 x 128 tiles everywhere: measured on MI355X, 256 x 256 tiles (one
+  // workgroup per CU) were no faster on any model shape.
+  p.big = 0;
   const int bm = p.big ? 256 : 128;
   p.tiles = (int)((int64_t)((M + bm - 1) / bm) * ((N + bm - 1) / bm));
   p.splits = 1;
@@ -365,23 +776,37 @@ template <int BM, int BN, int WM, int WN, bool AK, bool BK_, typename OutT>
 void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
   g.tiles = p.tiles;
   g.k_chunk = p.k_chunk;
+  // the v2 kernel addresses operands with 32-bit buffer offsets
+  const int64_t a_ext = (AK ? (int64_t)g.M + BM : (int64_t)g.K + BK) * g.lda * 2;
+  const int64_t b_ext = (BK_ ? (int64_t)g.N + BN : (int64_t)g.K + BK) * g.ldb * 2;
+  const bool v2 = WM == 2 && WN == 2 && a_ext < ((int64_t)1 << 31) && b_ext < ((int64_t)1 << 31);
+  // Pipeline choice measured on MI355X at the model's shapes: with both
+  // operands k-major (NT) 64-k stages win; otherwise 32-k stages (32 KB of LDS,
+  // more workgroups per CU to cover L2-miss latency) win.
+  auto launch2 = [&](int grid) {
+    if (AK && BK_) hipLaunchKernelGGL((gemm2_kernel<128, 128, 64, 2, AK, BK_, OutT>), dim3(grid), dim3(256), 0, st, g);
+    else hipLaunchKernelGGL((gemm2_kernel<128, 128, 32, 2, AK, BK_, OutT>), dim3(grid), dim3(256), 0, st, g);
+  };
   if (p.splits > 1) {
     g.ldw = p.ldw;  // g.ws already set by the caller
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles * p.splits), dim3(WM * WN * 64),
-                       0, st, g);
+    if (v2)
+      launch2(p.tiles * p.splits);
+    else
+      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles * p.splits), dim3(WM * WN * 64),
+                         0, st, g);
     const int64_t work = (int64_t)g.M * ((g.N + 3) / 4);
     const int blocks = (int)std::min<int64_t>((work + 255) / 256, 4096);
     hipLaunchKernelGGL((splitk_reduce_kernel<OutT>), dim3(blocks), dim3(256), 0, st, g, p.splits);
   } else {
     g.ws = nullptr;
-    hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles), dim3(WM * WN * 64), 0, st, g);
+    if (v2) launch2(p.tiles);
+    else hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles), dim3(WM * WN * 64), 0, st, g);
   }
 }
 
 template <bool AK, bool BK_, typename OutT>
 void launch_layout(const GemmArgs& g, const Plan& p, hipStream_t st) {
-  if (p.big) launch_cfg<256, 256, 2, 2, AK, BK_, OutT>(g, p, st);
-  else launch_cfg<128, 128, 2, 2, AK, BK_, OutT>(g, p, st);
+  launch_cfg<128, 128, 2, 2, AK, BK_, OutT>(g, p, st);
 }
 
 template <typename OutT>
