@@ -19,12 +19,14 @@ def bf16_bits(x) -> np.ndarray:
     model.py:372-375); this is that cast.
     """
     f = np.ascontiguousarray(np.asarray(x, dtype=np.float32))
-    u = f.view(np.uint32).astype(np.uint64)
+    u = f.view(np.uint32)
+    # finite values cannot overflow 32 bits here (largest is 0xFF7FFFFF + 0x8000);
+    # NaN patterns are replaced below
+    r = ((u + (np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1)))) >> 16).astype(np.uint16)
     nan = np.isnan(f)
-    lsb = (u >> 16) & 1
-    r = ((u + 0x7FFF + lsb) >> 16).astype(np.uint16)
-    r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
-    return r.astype(np.uint16)
+    if nan.any():
+        r = np.where(nan, ((u >> 16) | np.uint32(0x40)).astype(np.uint16), r)
+    return r
 
 
 def bf16_to_f32(bits) -> np.ndarray:

@@ -1,0 +1,109 @@
+"""CPU pins of the training-step oracle (oracle/model_np.py).
+
+The NumPy forward/backward is checked against float64 torch autograd of the
+same network written independently here (small configuration, no bf16
+rounding), AdamW against its closed form, and the schedule against optax's
+published formula at known points.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import model_np as om
+
+
+def _torch_loss(params, batch, cfg):
+    """Independent float64 restatement in torch (autograd supplies the backward)."""
+    ids = torch.from_numpy(batch[:, :-1]).long()
+    tg = torch.from_numpy(batch[:, 1:]).long()
+    bs, S = ids.shape
+    d, H = cfg.d, cfg.heads
+    dh = d // H
+    E = params["embeddings"]
+    x = E["token_embed"][ids] + E["pos_embed"][:S]
+    for b in params["blocks"]:
+        h = torch.nn.functional.layer_norm(x, (d,), b["ln1"]["gamma"], b["ln1"]["beta"], cfg.eps)
+        qkv = (h @ b["attn"]["W_qkv"]).view(bs, S, 3, H, dh)
+        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+        att = (q @ k.transpose(-1, -2)) / math.sqrt(dh)
+        att = att.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf")).softmax(-1)
+        o = (att @ v).transpose(1, 2).reshape(bs, S, d)
+        x = x + o @ b["attn"]["W_o"]
+        h2 = torch.nn.functional.layer_norm(x, (d,), b["ln2"]["gamma"], b["ln2"]["beta"], cfg.eps)
+        u = torch.nn.functional.gelu(h2 @ b["ffn"]["W1"] + b["ffn"]["b1"], approximate="tanh")
+        x = x + u @ b["ffn"]["W2"] + b["ffn"]["b2"]
+    hf = torch.nn.functional.layer_norm(x, (d,), params["ln_final"]["gamma"], params["ln_final"]["beta"], cfg.eps)
+    logits = hf @ params["lm_head"]
+    return torch.nn.functional.cross_entropy(logits.reshape(-1, cfg.vocab), tg.reshape(-1))
+
+
+def test_forward_backward_matches_float64_autograd():
+    cfg = om.Config(vocab=97, d=32, heads=4, layers=2, ff=64, max_seq=16)
+    p32 = om.init_params(3, cfg)
+    rng = np.random.default_rng(0)
+    # non-trivial LayerNorm parameters and biases so every gradient path is exercised
+    for b in p32["blocks"]:
+        for ln in ("ln1", "ln2"):
+            b[ln]["gamma"] += rng.standard_normal(32).astype(np.float32) * 0.1
+            b[ln]["beta"] += rng.standard_normal(32).astype(np.float32) * 0.1
+        b["ffn"]["b1"] += rng.standard_normal(64).astype(np.float32) * 0.1
+        b["ffn"]["b2"] += rng.standard_normal(32).astype(np.float32) * 0.1
+    p64 = om._map(lambda a: a.astype(np.float64), p32)
+    batch = rng.integers(0, cfg.vocab, (3, 13)).astype(np.int64)
+    loss, grads = om.loss_and_grads(p64, batch, cfg, exact=True)
+    tp = om._map(lambda a: torch.from_numpy(a.copy()).requires_grad_(True), p64)
+    tl = _torch_loss(tp, batch, cfg)
+    tl.backward()
+    assert abs(loss - tl.item()) < 1e-10
+    for g, t in zip(om._leaves(grads), om._leaves(tp)):
+        np.testing.assert_allclose(g, t.grad.numpy(), rtol=1e-7, atol=1e-10)
+
+
+def test_rounded_forward_stays_close_to_exact():
+    cfg = om.Config(vocab=97, d=32, heads=4, layers=2, ff=64, max_seq=16)
+    p = om.init_params(1, cfg)
+    batch = np.random.default_rng(1).integers(0, cfg.vocab, (2, 9))
+    l_exact, _ = om.loss_and_grads(p, batch, cfg, exact=True)
+    l_bf16, _ = om.loss_and_grads(p, batch, cfg)
+    assert abs(l_exact - l_bf16) < 5e-3
+    assert abs(l_exact - math.log(cfg.vocab)) < 0.1   # tiny weights -> near-uniform prediction
+
+
+def test_adamw_closed_form_first_steps():
+    p = {"w": np.array([1.0], np.float64)}
+    opt = om.AdamWNP(p, lambda c: 0.1, wd=0.5)
+    g = {"w": np.array([2.0])}
+    opt.step(p, g)
+    # step 1: m = .1 g, v = .001 g^2, mhat = g, vhat = g^2 -> update sign(g) + wd * p
+    assert p["w"][0] == pytest.approx(1.0 - 0.1 * (2.0 / (2.0 + 1e-8) + 0.5 * 1.0), rel=1e-12)
+
+
+def test_warmup_cosine_schedule_known_points():
+    f = lambda c: om.warmup_cosine(c, 1e-3, 200, 1000, 1e-4)
+    assert f(0) == 0.0
+    assert f(100) == pytest.approx(5e-4)
+    assert f(200) == pytest.approx(1e-3)
+    assert f(600) == pytest.approx(1e-4 + 0.9e-3 * 0.5)      # half way down the cosine
+    assert f(1000) == pytest.approx(1e-4)
+    assert f(5000) == pytest.approx(1e-4)
+
+
+def test_device_schedule_matches_oracle_schedule():
+    from nlearn_amd.train import warmup_cosine_decay_schedule
+
+    s = warmup_cosine_decay_schedule(0.0, 1e-3, 200, 1000, 1e-4)
+    for c in (0, 1, 57, 199, 200, 201, 555, 999, 1000, 1234):
+        assert s(c) == pytest.approx(om.warmup_cosine(c, 1e-3, 200, 1000, 1e-4), rel=1e-12, abs=1e-15)
+
+
+def test_init_matches_device_initialiser():
+    from nlearn_amd.model import ModelConfig, init_params_numpy, tree_leaves
+
+    cfg = ModelConfig(vocab_size=97, d_model=32, n_heads=4, n_layers=2, d_ff=64, max_seq_len=16)
+    a = tree_leaves(init_params_numpy(5, cfg))
+    b = om._leaves(om.init_params(5, om.Config(vocab=97, d=32, heads=4, layers=2, ff=64, max_seq=16)))
+    assert len(a) == len(b)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)

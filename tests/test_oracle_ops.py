@@ -1,0 +1,116 @@
+"""CPU pins of the op-level oracle (oracle/ops.py) against independent
+implementations and closed forms. Each check is chosen so that a plausible
+mistake (a dropped term, a wrong sign or index, a transposed operand) fails."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ops
+
+
+def test_bf16_rounding_matches_torch_bit_for_bit():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(200000).astype(np.float32) * 10,
+                        np.array([0.0, -0.0, 1e-40, -1e-40, 3.3895e38, -3.3895e38, np.inf, -np.inf], np.float32),
+                        # exact ties: RNE must pick the even neighbour
+                        (np.arange(1, 1000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)])
+    ref = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ops.bf16_bits(x), ref)
+    nan = ops.bf16_to_f32(ops.bf16_bits(np.array([np.nan], np.float32)))
+    assert np.isnan(nan[0])
+
+
+@pytest.mark.parametrize("opA,opB", [("N", "N"), ("N", "T"), ("T", "N"), ("T", "T")])
+def test_gemm_transposes_and_exact_integers(opA, opB):
+    rng = np.random.default_rng(1)
+    A = rng.integers(-4, 5, (37, 53)).astype(np.float32)
+    B = rng.integers(-4, 5, (53, 29)).astype(np.float32)
+    ref = A.astype(np.int64) @ B.astype(np.int64)     # exact integer product
+    As = A.T.copy() if opA == "T" else A
+    Bs = B.T.copy() if opB == "T" else B
+    assert np.array_equal(ops.gemm(As, Bs, opA, opB), ref)
+
+
+def _torch_attention(q, k, v, causal):
+    s = q @ k.transpose(-1, -2) / math.sqrt(q.shape[-1])
+    if causal:
+        S = q.shape[1]
+        s = s.masked_fill(torch.triu(torch.ones(S, S, dtype=torch.bool), 1), float("-inf"))
+    return torch.softmax(s, -1) @ v, torch.logsumexp(s, -1)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("n,s,d", [(2, 16, 8), (3, 37, 64)])
+def test_flash_forward_backward_vs_float64_autograd(n, s, d, causal):
+    rng = np.random.default_rng(n * s + d)
+    Q, K, V, dO = (rng.standard_normal((n, s, d)) for _ in range(4))
+    O, L = ops.flash_fwd(Q, K, V, causal=causal)
+    dQ, dK, dV, D = ops.flash_bwd(Q, K, V, dO, causal=causal)
+    tq, tk, tv = (torch.from_numpy(a).requires_grad_(True) for a in (Q, K, V))
+    tO, tL = _torch_attention(tq, tk, tv, causal)
+    tO.backward(torch.from_numpy(dO))
+    np.testing.assert_allclose(O, tO.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(L, tL.detach().numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dQ, tq.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dK, tk.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dV, tv.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(D, (dO * O).sum(-1), rtol=1e-12)
+
+
+def test_flash_closed_forms_and_invariants():
+    rng = np.random.default_rng(5)
+    n, s, d = 2, 24, 16
+    Q, K, V, dO = (rng.standard_normal((n, s, d)) for _ in range(4))
+    O, L = ops.flash_fwd(Q, K, V)
+    # the first query sees only the first key
+    np.testing.assert_allclose(O[:, 0], V[:, 0], rtol=1e-12)
+    np.testing.assert_allclose(L[:, 0], (Q[:, 0] * K[:, 0]).sum(-1) / math.sqrt(d), rtol=1e-12)
+    # identical keys -> uniform weights over the causal prefix -> prefix mean of V
+    Ke = np.repeat(K[:, :1], s, axis=1)
+    Oe, _ = ops.flash_fwd(Q, Ke, V)
+    prefix_mean = np.cumsum(V, 1) / np.arange(1, s + 1)[None, :, None]
+    np.testing.assert_allclose(Oe, prefix_mean, rtol=1e-10, atol=1e-12)
+    dQ, dK, dV, _ = ops.flash_bwd(Q, K, V, dO)
+    np.testing.assert_allclose(dV.sum(1), dO.sum(1), rtol=1e-10)      # rows of P sum to 1
+    np.testing.assert_allclose(dK.sum(1), 0.0, atol=1e-10)            # softmax shift invariance
+    # finite differences on one entry of K
+    eps = 1e-6
+    K2 = K.copy()
+    K2[1, 3, 5] += eps
+    O2, _ = ops.flash_fwd(Q, K2, V)
+    fd = ((O2 - O) * dO).sum() / eps
+    assert fd == pytest.approx(dK[1, 3, 5], rel=1e-4, abs=1e-7)
+
+
+def test_flash_never_uses_future_keys():
+    rng = np.random.default_rng(6)
+    Q, K, V = (rng.standard_normal((1, 10, 8)) for _ in range(3))
+    K2, V2 = K.copy(), V.copy()
+    K2[:, 6:] = 1e6
+    V2[:, 6:] = -1e6
+    O1, L1 = ops.flash_fwd(Q, K, V)
+    O2, L2 = ops.flash_fwd(Q, K2, V2)
+    np.testing.assert_allclose(O1[:, :6], O2[:, :6], rtol=1e-12)
+    np.testing.assert_allclose(L1[:, :6], L2[:, :6], rtol=1e-12)
+
+
+def test_ce_vs_torch_and_invariants():
+    rng = np.random.default_rng(7)
+    M, V = 33, 101
+    x = rng.standard_normal((M, V)) * 3
+    t = rng.integers(0, V, M)
+    loss, lse, dl = ops.ce(x, t)
+    tx = torch.from_numpy(x).requires_grad_(True)
+    tl = torch.nn.functional.cross_entropy(tx, torch.from_numpy(t))
+    tl.backward()
+    assert loss.mean() == pytest.approx(tl.item(), rel=1e-12)
+    np.testing.assert_allclose(dl, tx.grad.numpy(), rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(lse, torch.logsumexp(torch.from_numpy(x), -1).numpy(), rtol=1e-12)
+    np.testing.assert_allclose(dl.sum(1), 0.0, atol=1e-14)
+    assert (dl[np.arange(M), t] < 0).all() and (np.delete(dl.ravel(), np.arange(M) * V + t) > 0).all()
+    assert (loss >= 0).all()
+    # uniform logits give exactly ln V
+    l0, _, _ = ops.ce(np.zeros((4, V)), np.arange(4))
+    np.testing.assert_allclose(l0, math.log(V), rtol=1e-14)
