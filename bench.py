@@ -48,9 +48,10 @@ class KernelProbe:
 
     @staticmethod
     def tag(name, args):
-        if name in ("nl_gemm", "nl_gemm_ex"):
+        if name in ("nl_gemm", "nl_gemm_ex", "nl_gemm_fused"):
             opA, opB, M, N, K = args[1:6]
-            return f"gemm_{'NT'[opA]}{'NT'[opB]}_{M}x{N}x{K}", 2.0 * M * N * K, "flops"
+            epi = ("", "_bias", "_bias_gelu", "_dgelu")[args[16]] if name == "nl_gemm_fused" else ""
+            return f"gemm_{'NT'[opA]}{'NT'[opB]}_{M}x{N}x{K}{epi}", 2.0 * M * N * K, "flops"
         if name == "nl_ce_fwd_bwd":
             M, V = args[1:3]
             return f"ce_fwd_bwd_{M}x{V}", 4.0 * M * V + 12.0 * M, "bytes"

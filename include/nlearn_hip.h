@@ -96,6 +96,31 @@ int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K,
                float beta, void* C, int c_dtype, int64_t ldc,
                const float* alpha_dev, void* ws, size_t ws_bytes);
 
+/* nl_gemm_ex with a fused output stage applied to v = alpha * s * op(A).op(B)
+ * before C is written (and, when K is split, after the ordered reduction):
+ *   NL_EPI_NONE       C = v + beta * C                       (= nl_gemm_ex)
+ *   NL_EPI_BIAS       C = v + bias[n] + beta * C
+ *   NL_EPI_BIAS_GELU  u = bf16(v + bias[n]); aux[m][n] = u; C = gelu_tanh(u)
+ *   NL_EPI_DGELU      C = v * gelu_tanh'(aux[m][n])          (aux = the u saved above)
+ * bias is fp32 [N], 16-byte aligned; aux is bf16 [M][ldaux], 16-byte aligned,
+ * ldaux >= N and a multiple of 8; the GELU forms need beta == 0.
+ * gelu_tanh(u) = u/2 (1 + tanh(sqrt(2/pi) (u + 0.044715 u^3))).
+ *
+ * Replaces the XLA-fused elementwise work around linear() in the FFN,
+ * model.py:266-277 (linear -> activation -> linear) and its autodiff; the
+ * benchmark layout uses the tanh-GELU with biases b1, b2 in place of the
+ * current SwiGLU gate. */
+#define NL_EPI_NONE      0
+#define NL_EPI_BIAS      1
+#define NL_EPI_BIAS_GELU 2
+#define NL_EPI_DGELU     3
+int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K,
+                  float alpha, const nl_bf16* A, int64_t lda,
+                  const nl_bf16* B, int64_t ldb,
+                  float beta, void* C, int c_dtype, int64_t ldc,
+                  const float* alpha_dev, int epi, const float* bias,
+                  nl_bf16* aux, int64_t ldaux, void* ws, size_t ws_bytes);
+
 /* ======================================================================== */
 /* Causal FlashAttention (head dim 64)                                        */
 /* ======================================================================== */
@@ -237,6 +262,57 @@ int nl_scale_bf16_by_device_scalar(void* stream, nl_bf16* x, int64_t rows, int64
 int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const float* g, float* m, float* v,
                   nl_bf16* p_bf16, int64_t ld_bf16, float lr, float b1, float b2, float eps, float wd,
                   float bc1, float bc2);
+
+/* ======================================================================== */
+/* LayerNorm, bias gradients, embedding                                       */
+/* ======================================================================== */
+/*
+ * LayerNorm over rows of a bf16 [rows][D] matrix (dense, D % 8 == 0, D <= 4096),
+ * fp32 gamma / beta / statistics:
+ *   s = x (+ residual; then s is rounded to bf16 and written to sum_out)
+ *   y = bf16((s - mean) * rstd * gamma + beta),  rstd = 1 / sqrt(var(s) + eps)
+ * mean and rstd ([rows] fp32) are saved for the backward. Folding the residual
+ * add of the block into the next LayerNorm reads the residual stream once.
+ * All pointers 16-byte aligned.
+ *
+ * Replaces layer_norm (model.py:228-241) and the residual adds of
+ * block_forward (model.py:315-324); the benchmark layout normalises with a
+ * mean-centred LayerNorm with learned beta (the current file uses RMSNorm).
+ */
+int nl_layernorm_fwd(void* stream, int rows, int D, const nl_bf16* x, const nl_bf16* residual,
+                     nl_bf16* sum_out, const float* gamma, const float* beta, float eps,
+                     nl_bf16* y, float* mean, float* rstd);
+
+/* Backward of nl_layernorm_fwd (the autodiff of model.py:228-241):
+ *   dx = rstd * (g - mean(g) - xh * mean(g * xh)) (+ dres),  g = dy * gamma,
+ *   xh = (x - mean) * rstd, with x the normalised input (sum_out when fused);
+ *   dgamma (+)= sum_rows dy * xh,  dbeta (+)= sum_rows dy   (accumulate != 0 adds).
+ * dres (may be NULL) is the gradient arriving through the residual branch.
+ * The parameter sums use a workspace of nl_layernorm_bwd_ws_bytes() bytes and
+ * are reduced in a fixed order (bitwise reproducible). */
+size_t nl_layernorm_bwd_ws_bytes(int rows, int D);
+int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x,
+                     const float* mean, const float* rstd, const float* gamma, const nl_bf16* dres,
+                     nl_bf16* dx, float* dgamma, float* dbeta, int accumulate, void* ws, size_t ws_bytes);
+
+/* out[c] (+)= sum_r x[r][c] over a bf16 [rows][ld] matrix: the bias gradients
+ * db = sum_rows dY of the FFN biases (autodiff of model.py:266-277 with the
+ * benchmark's b1, b2). Fixed summation order; workspace nl_colsum_ws_bytes(). */
+size_t nl_colsum_ws_bytes(int rows, int cols);
+int nl_colsum_bf16(void* stream, int rows, int cols, const nl_bf16* x, int64_t ld, float* out,
+                   int accumulate, void* ws, size_t ws_bytes);
+
+/* out[b][s][:] = bf16(tok[ids[b][s]][:] + pos[s][:]), fp32 tables [vocab][D] and
+ * [>= seq][D], D % 4 == 0; an id outside [0, vocab) gives a NaN row.
+ * Replaces embed (model.py:75-85) with the benchmark's learned position table. */
+int nl_embedding_fwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
+                     const float* tok, const float* pos, nl_bf16* out);
+
+/* dtok[ids[t]] += dx[t] (fp32 atomics: the caller zeroes dtok; repeated ids are
+ * summed in hardware order), dpos[s] (+)= sum_b dx[b][s] in batch order.
+ * The autodiff of the gather in model.py:75-85. */
+int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
+                     const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos);
 
 #ifdef __cplusplus
 }

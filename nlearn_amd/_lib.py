@@ -43,6 +43,8 @@ _SIGNATURES = {
     "nl_gemm": [_P, _I, _I, _I, _I, _I, _F, _P, _I64, _P, _I64, _F, _P, _I, _I64, _P],
     "nl_gemm_ws_bytes": [_I, _I, _I, _I, _I],
     "nl_gemm_ex": [_P, _I, _I, _I, _I, _I, _F, _P, _I64, _P, _I64, _F, _P, _I, _I64, _P, _P, ctypes.c_size_t],
+    "nl_gemm_fused": [_P, _I, _I, _I, _I, _I, _F, _P, _I64, _P, _I64, _F, _P, _I, _I64, _P, _I, _P, _P, _I64, _P,
+                      ctypes.c_size_t],
     "nl_flash_attention_fwd": [_P, _I, _I, _I, _I, _F, _I, _P, _S, _P, _S, _P, _S, _P, _S, _P],
     "nl_flash_attention_bwd_preprocess": [_P, _I, _I, _I, _I, _P, _S, _P, _S, _P],
     "nl_flash_attention_bwd_dq": [_P, _I, _I, _I, _I, _F, _I, _P, _S, _P, _S, _P, _S, _P, _S, _P, _P, _P, _S],
@@ -57,6 +59,13 @@ _SIGNATURES = {
     "nl_mean_f32": [_P, _P, _I, _P],
     "nl_scale_bf16_by_device_scalar": [_P, _P, _I64, _I64, _I64, _P],
     "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F],
+    "nl_layernorm_fwd": [_P, _I, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P],
+    "nl_layernorm_bwd_ws_bytes": [_I, _I],
+    "nl_layernorm_bwd": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t],
+    "nl_colsum_ws_bytes": [_I, _I],
+    "nl_colsum_bf16": [_P, _I, _I, _P, _I64, _P, _I, _P, ctypes.c_size_t],
+    "nl_embedding_fwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
+    "nl_embedding_bwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I],
 }
 _RESTYPES = {
     "nl_strerror": ctypes.c_char_p,
@@ -64,6 +73,8 @@ _RESTYPES = {
     "nl_version": ctypes.c_char_p,
     "nl_flash_attention_bwd_ws_bytes": ctypes.c_size_t,
     "nl_gemm_ws_bytes": ctypes.c_size_t,
+    "nl_layernorm_bwd_ws_bytes": ctypes.c_size_t,
+    "nl_colsum_ws_bytes": ctypes.c_size_t,
 }
 
 EXPORTED = tuple(_SIGNATURES)

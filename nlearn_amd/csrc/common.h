@@ -50,6 +50,33 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 // ---------------------------------------------------------------------------
+// tanh-approximated GELU (the FFN activation) and its derivative, in the
+// equivalent logistic form (1 + tanh(z)) / 2 = sigmoid(2z):
+//   gelu(u)  = u * s,  s = 1 / (1 + 2^(u (k1 + k2 u^2))),
+//              k1 = -2 c log2(e), k2 = -2 c a log2(e),  c = sqrt(2/pi), a = 0.044715
+//   gelu'(u) = s * (1 + u (1 - s) (2c + 6ca u^2))
+// One v_exp_f32 and one v_rcp_f32 per element, no IEEE divide. Saturation:
+// 2^(+inf) = inf gives s = 0 and 2^(-inf) = 0 gives s = 1, so gelu is exact at
+// both ends; the derivative clamps |u| <= 20, beyond which it is 0 or 1 in fp32.
+// ---------------------------------------------------------------------------
+constexpr float kGeluK1 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+constexpr float kGeluK2 = kGeluK1 * 0.044715f;
+constexpr float kGeluD1 = 2.0f * 0.7978845608028654f;
+constexpr float kGeluD2 = 6.0f * 0.7978845608028654f * 0.044715f;
+__device__ __forceinline__ float gelu_sigmoid_arg(float u) {
+  return 1.f + fast_exp2(u * __builtin_fmaf(kGeluK2, u * u, kGeluK1));
+}
+__device__ __forceinline__ float gelu_tanh(float u) {
+  return u * __builtin_amdgcn_rcpf(gelu_sigmoid_arg(u));
+}
+__device__ __forceinline__ float gelu_tanh_grad(float u) {
+  u = fminf(fmaxf(u, -20.f), 20.f);
+  const float s = __builtin_amdgcn_rcpf(gelu_sigmoid_arg(u));
+  const float q = __builtin_fmaf(kGeluD2, u * u, kGeluD1);
+  return s * __builtin_fmaf(u * (1.f - s), q, 1.f);
+}
+
+// ---------------------------------------------------------------------------
 // wavefront reductions (butterfly over all 64 lanes)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float wave_max(float v) {

@@ -1,0 +1,429 @@
+// fused.hip — the elementwise tail of the training step around the GEMMs:
+// LayerNorm (forward with the residual add folded in, backward with the
+// residual gradient folded in), column sums for bias gradients, and the token
+// + learned-position embedding (forward and backward).
+//
+// Math (nlearn/model.py:216-241 normalisation params and call, model.py:315-324
+// pre-norm residual blocks, model.py:75-86 embedding lookup; the LayerNorm with
+// gamma/beta and the learned position table are the layout the benchmark
+// configuration trains):
+//   LN:   y = (x - mean) * rstd * gamma + beta,  rstd = 1/sqrt(var + eps)
+//   dLN:  dx = rstd * (g - mean(g) - xh * mean(g * xh)),  g = dy * gamma, xh = (x - mean) * rstd
+//         dgamma = sum_rows dy * xh,  dbeta = sum_rows dy
+//
+// MI355X design: one 64-lane wave per row (a 512-wide bf16 row is one 16-byte
+// vector per lane), wavefront butterflies for the row statistics, no LDS in
+// the forward. Parameter-gradient sums are per-workgroup partial rows combined
+// in a fixed order by a second kernel (deterministic, no atomics).
+#include "common.h"
+
+namespace nl {
+namespace {
+
+constexpr int kRowsPerBlock = 4;   // LayerNorm: one wave per row, 4 waves per workgroup
+constexpr int kMaxD = 4096;        // LayerNorm width limit (8 vectors of 8 per lane)
+constexpr int kLnBwdBlocks = 1024; // LayerNorm backward: partial rows of dgamma / dbeta
+constexpr int kColsumRows = 64;    // column sums: rows per partial
+
+// Lane `lane` holds columns (i*64 + lane)*8 .. +7 of the row in vector i.
+template <int VPL>
+__device__ __forceinline__ void load_row(u32x4 (&v)[VPL], const uint16_t* p, int D, int lane) {
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    v[i] = (c < D) ? *reinterpret_cast<const u32x4*>(p + c) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ void unpack8(const u32x4& v, float f[8]) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    f[2 * q] = bf16_lo(v[q]);
+    f[2 * q + 1] = bf16_hi(v[q]);
+  }
+}
+__device__ __forceinline__ u32x4 pack8(const float f[8]) {
+  u32x4 v;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) v[q] = pack_bf16x2(f[2 * q], f[2 * q + 1]);
+  return v;
+}
+__device__ __forceinline__ void load8f(const float* p, float f[8]) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p), b = *reinterpret_cast<const f32x4*>(p + 4);
+  f[0] = a[0], f[1] = a[1], f[2] = a[2], f[3] = a[3], f[4] = b[0], f[5] = b[1], f[6] = b[2], f[7] = b[3];
+}
+
+// y = LN(s), s = x (+ r). With r, s is rounded to bf16 and stored to s_out (the
+// residual stream the next block reads) before it is normalised.
+template <int VPL>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, int D, const uint16_t* __restrict__ x,
+                                                                    const uint16_t* __restrict__ r,
+                                                                    uint16_t* __restrict__ s_out,
+                                                                    const float* __restrict__ gamma,
+                                                                    const float* __restrict__ beta,
+                                                                    uint16_t* __restrict__ y, float* __restrict__ mean_out,
+                                                                    float* __restrict__ rstd_out, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int64_t off = (int64_t)row * D;
+  u32x4 xv[VPL];
+  load_row<VPL>(xv, x + off, D, lane);
+  float f[VPL][8];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) unpack8(xv[i], f[i]);
+  if (r) {
+    u32x4 rv[VPL];
+    load_row<VPL>(rv, r + off, D, lane);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float g[8];
+      unpack8(rv[i], g);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) f[i][j] = bf16_to_f32(f32_to_bf16(f[i][j] + g[j]));
+      const int c = (i * 64 + lane) * 8;
+      if (c < D) *reinterpret_cast<u32x4*>(s_out + off + c) = pack8(f[i]);
+    }
+  }
+  // columns beyond D hold zeros, so they add nothing to the sum
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += f[i][j];
+  const float mean = wave_sum(s) / (float)D;
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const bool in = (i * 64 + lane) * 8 < D;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float d = in ? f[i][j] - mean : 0.f;
+      v += d * d;
+    }
+  }
+  const float rstd = rsqrtf(wave_sum(v) / (float)D + eps);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c >= D) continue;
+    float gg[8], bb[8], o[8];
+    load8f(gamma + c, gg);
+    load8f(beta + c, bb);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = (f[i][j] - mean) * rstd * gg[j] + bb[j];
+    *reinterpret_cast<u32x4*>(y + off + c) = pack8(o);
+  }
+  if (lane == 0) {
+    mean_out[row] = mean;
+    rstd_out[row] = rstd;
+  }
+}
+
+// dx = dLN(dy) (+ dres). Each workgroup also writes one partial row of dgamma
+// and one of dbeta (its 4 waves combined in wave order).
+template <int VPL>
+__global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
+    int rows, int D, const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const float* __restrict__ mean_in,
+    const float* __restrict__ rstd_in, const float* __restrict__ gamma, const uint16_t* __restrict__ dres,
+    uint16_t* __restrict__ dx, float* __restrict__ part_g, float* __restrict__ part_b) {
+  __shared__ float sg[VPL * 512];
+  __shared__ float sb[VPL * 512];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float ag[VPL][8], ab[VPL][8], gam[VPL][8];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ag[i][j] = ab[i][j] = gam[i][j] = 0.f;
+    if (c < D) load8f(gamma + c, gam[i]);
+  }
+  for (int row = blockIdx.x * kRowsPerBlock + wave; row < rows; row += gridDim.x * kRowsPerBlock) {
+    const int64_t off = (int64_t)row * D;
+    u32x4 dv[VPL], xv[VPL];
+    load_row<VPL>(dv, dy + off, D, lane);
+    load_row<VPL>(xv, x + off, D, lane);
+    const float mu = mean_in[row], rs = rstd_in[row];
+    float g[VPL][8], xh[VPL][8];
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float dyf[8], xf[8];
+      unpack8(dv[i], dyf);
+      unpack8(xv[i], xf);
+      const bool in = (i * 64 + lane) * 8 < D;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        xh[i][j] = in ? (xf[j] - mu) * rs : 0.f;
+        g[i][j] = dyf[j] * gam[i][j];
+        s1 += g[i][j];
+        s2 += g[i][j] * xh[i][j];
+        ag[i][j] += dyf[j] * xh[i][j];
+        ab[i][j] += dyf[j];
+      }
+    }
+    const float m1 = wave_sum(s1) / (float)D, m2 = wave_sum(s2) / (float)D;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int c = (i * 64 + lane) * 8;
+      if (c >= D) continue;
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = rs * (g[i][j] - m1 - xh[i][j] * m2);
+      if (dres) {
+        float rf[8];
+        unpack8(*reinterpret_cast<const u32x4*>(dres + off + c), rf);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] += rf[j];
+      }
+      *reinterpret_cast<u32x4*>(dx + off + c) = pack8(o);
+    }
+  }
+  // combine the 4 waves in wave order (deterministic), one partial row per workgroup
+  for (int w = 0; w < kRowsPerBlock; ++w) {
+    if (wave == w) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int c = (i * 64 + lane) * 8 + j;
+          sg[c] = (w == 0 ? 0.f : sg[c]) + ag[i][j];
+          sb[c] = (w == 0 ? 0.f : sb[c]) + ab[i][j];
+        }
+    }
+    __syncthreads();
+  }
+  for (int c = threadIdx.x; c < D; c += blockDim.x) {
+    part_g[(int64_t)blockIdx.x * D + c] = sg[c];
+    part_b[(int64_t)blockIdx.x * D + c] = sb[c];
+  }
+}
+
+// out[c] (+)= sum_{p<P} part[p][c], summed in a fixed order: thread group ty
+// takes p = ty, ty+16, ..., then the 16 group sums are added in ty order.
+// Block: 64 columns x 16 groups.
+__global__ __launch_bounds__(1024) void sum_partials_kernel(int P, int D, const float* __restrict__ part,
+                                                            float* __restrict__ out, int accumulate) {
+  __shared__ float s[16][64];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + tx;
+  float a = 0.f;
+  if (c < D) {
+#pragma unroll 8
+    for (int p = ty; p < P; p += 16) a += part[(int64_t)p * D + c];
+  }
+  s[ty][tx] = a;
+  __syncthreads();
+  if (ty == 0 && c < D) {
+    float t = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t += s[k][tx];
+    out[c] = accumulate ? out[c] + t : t;
+  }
+}
+
+// Partial column sums of a bf16 [rows][cols] matrix (row stride ld, ld % 8 == 0):
+// workgroup (bx, by) sums rows [by*kColsumRows, +kColsumRows) of columns
+// [bx*512, +512). 64 lanes x 8 columns, 4 row phases combined in order.
+__global__ __launch_bounds__(256) void colsum_partial_kernel(int rows, int cols, const uint16_t* __restrict__ x,
+                                                             int64_t ld, float* __restrict__ part) {
+  __shared__ float s[4][512];
+  const int lane = threadIdx.x & 63, ph = threadIdx.x >> 6;
+  const int c = blockIdx.x * 512 + lane * 8;
+  const int r0 = blockIdx.y * kColsumRows;
+  const int r1 = min(rows, r0 + kColsumRows);
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (c < cols) {
+    if (c + 8 <= cols) {
+#pragma unroll 4
+      for (int r = r0 + ph; r < r1; r += 4) {
+        float f[8];
+        unpack8(*reinterpret_cast<const u32x4*>(x + (int64_t)r * ld + c), f);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) a[j] += f[j];
+      }
+    } else {
+      for (int r = r0 + ph; r < r1; r += 4)
+        for (int j = 0; j < cols - c; ++j) a[j] += bf16_to_f32(x[(int64_t)r * ld + c + j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s[ph][lane * 8 + j] = a[j];
+  __syncthreads();
+  for (int k = threadIdx.x; k < 512; k += 256) {
+    const int cc = blockIdx.x * 512 + k;
+    if (cc < cols) part[(int64_t)blockIdx.y * cols + cc] = ((s[0][k] + s[1][k]) + s[2][k]) + s[3][k];
+  }
+}
+
+// out[t, :] = bf16(tok[ids[t]] + pos[t % S])  (fp32 tables, D % 4 == 0).
+// An id outside [0, vocab) yields a NaN row.
+__global__ __launch_bounds__(128) void embed_fwd_kernel(int S, int D, const int32_t* __restrict__ ids,
+                                                        const float* __restrict__ tok, const float* __restrict__ pos,
+                                                        uint16_t* __restrict__ out, int vocab) {
+  const int t = blockIdx.x;
+  const int s = t % S;
+  const int id = ids[t];
+  const bool ok = id >= 0 && id < vocab;
+  for (int c = threadIdx.x * 4; c < D; c += 128 * 4) {
+    const f32x4 a = ok ? *reinterpret_cast<const f32x4*>(tok + (int64_t)id * D + c) : f32x4{NAN, NAN, NAN, NAN};
+    const f32x4 p = *reinterpret_cast<const f32x4*>(pos + (int64_t)s * D + c);
+    *reinterpret_cast<u32x2*>(out + (int64_t)t * D + c) =
+        u32x2{pack_bf16x2(a[0] + p[0], a[1] + p[1]), pack_bf16x2(a[2] + p[2], a[3] + p[3])};
+  }
+}
+
+// dtok[ids[t]] += dx[t] with fp32 atomics (rows of repeated tokens are summed in
+// hardware order, the one non-deterministic sum of the step); ids outside
+// [0, vocab) contribute nothing.
+__global__ __launch_bounds__(128) void embed_bwd_tok_kernel(int D, const int32_t* __restrict__ ids,
+                                                            const uint16_t* __restrict__ dx, float* __restrict__ dtok,
+                                                            int vocab) {
+  const int t = blockIdx.x;
+  const int id = ids[t];
+  if (id < 0 || id >= vocab) return;
+  for (int c = threadIdx.x; c < D; c += 128)
+    atomicAdd(dtok + (int64_t)id * D + c, bf16_to_f32(dx[(int64_t)t * D + c]));
+}
+
+// dpos[s] (+)= sum_b dx[b, s] in batch order.
+__global__ __launch_bounds__(128) void embed_bwd_pos_kernel(int B, int S, int D, const uint16_t* __restrict__ dx,
+                                                            float* __restrict__ dpos, int accumulate) {
+  const int s = blockIdx.x;
+  for (int c = threadIdx.x; c < D; c += 128) {
+    float a = 0.f;
+    for (int b = 0; b < B; ++b) a += bf16_to_f32(dx[((int64_t)b * S + s) * D + c]);
+    float* o = dpos + (int64_t)s * D + c;
+    *o = accumulate ? *o + a : a;
+  }
+}
+
+int vectors_per_lane(int D) {
+  const int v = (D + 511) / 512;
+  return v <= 1 ? 1 : v <= 2 ? 2 : v <= 4 ? 4 : 8;
+}
+
+int ln_bwd_blocks(int rows) { return std::min(kLnBwdBlocks, (rows + kRowsPerBlock - 1) / kRowsPerBlock); }
+
+}  // namespace
+}  // namespace nl
+
+using namespace nl;
+
+extern "C" int nl_layernorm_fwd(void* stream, int rows, int D, const nl_bf16* x, const nl_bf16* residual,
+                                nl_bf16* sum_out, const float* gamma, const float* beta, float eps, nl_bf16* y,
+                                float* mean, float* rstd) {
+  if (rows < 0 || D <= 0 || (D % 8) != 0 || D > kMaxD)
+    return nl_set_error(NL_EINVAL, "layernorm: need 0 < D <= 4096 and D % 8 == 0");
+  if (rows == 0) return NL_OK;
+  if (!x || !gamma || !beta || !y || !mean || !rstd || (residual && !sum_out))
+    return nl_set_error(NL_EINVAL, "layernorm: null pointer");
+  if ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)residual | (uintptr_t)sum_out) &
+       15) != 0)
+    return nl_set_error(NL_EALIGN, "layernorm: buffers must be 16-byte aligned");
+  dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(64 * kRowsPerBlock);
+  hipStream_t st = (hipStream_t)stream;
+  switch (vectors_per_lane(D)) {
+#define NL_LNF(N)                                                                                                    \
+  case N:                                                                                                            \
+    hipLaunchKernelGGL(ln_fwd_kernel<N>, grid, block, 0, st, rows, D, x, residual, sum_out, gamma, beta, y, mean, rstd, \
+                       eps);                                                                                         \
+    break;
+    NL_LNF(1)
+    NL_LNF(2)
+    NL_LNF(4)
+    NL_LNF(8)
+#undef NL_LNF
+  }
+  return nl_check_launch("nl_layernorm_fwd");
+}
+
+extern "C" size_t nl_layernorm_bwd_ws_bytes(int rows, int D) {
+  if (rows <= 0 || D <= 0) return 0;
+  return (size_t)2 * ln_bwd_blocks(rows) * D * sizeof(float);
+}
+
+extern "C" int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x, const float* mean,
+                                const float* rstd, const float* gamma, const nl_bf16* dres, nl_bf16* dx, float* dgamma,
+                                float* dbeta, int accumulate, void* ws, size_t ws_bytes) {
+  if (rows < 0 || D <= 0 || (D % 8) != 0 || D > kMaxD)
+    return nl_set_error(NL_EINVAL, "layernorm: need 0 < D <= 4096 and D % 8 == 0");
+  if (rows == 0) return NL_OK;
+  if (!dy || !x || !mean || !rstd || !gamma || !dx || !dgamma || !dbeta || !ws)
+    return nl_set_error(NL_EINVAL, "layernorm_bwd: null pointer");
+  if ((((uintptr_t)dy | (uintptr_t)x | (uintptr_t)dx | (uintptr_t)dres | (uintptr_t)gamma | (uintptr_t)ws) & 15) != 0)
+    return nl_set_error(NL_EALIGN, "layernorm_bwd: buffers must be 16-byte aligned");
+  if (ws_bytes < nl_layernorm_bwd_ws_bytes(rows, D))
+    return nl_set_error(NL_EINVAL, "layernorm_bwd: workspace smaller than nl_layernorm_bwd_ws_bytes()");
+  const int blocks = ln_bwd_blocks(rows);
+  float* pg = static_cast<float*>(ws);
+  float* pb = pg + (size_t)blocks * D;
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid(blocks), block(64 * kRowsPerBlock);
+  switch (vectors_per_lane(D)) {
+#define NL_LNB(N)                                                                                                       \
+  case N:                                                                                                               \
+    hipLaunchKernelGGL(ln_bwd_kernel<N>, grid, block, 0, st, rows, D, dy, x, mean, rstd, gamma, dres, dx, pg, pb); \
+    break;
+    NL_LNB(1)
+    NL_LNB(2)
+    NL_LNB(4)
+    NL_LNB(8)
+#undef NL_LNB
+  }
+  const dim3 rg((D + 63) / 64);
+  hipLaunchKernelGGL(sum_partials_kernel, rg, dim3(1024), 0, st, blocks, D, (const float*)pg, dgamma, accumulate);
+  hipLaunchKernelGGL(sum_partials_kernel, rg, dim3(1024), 0, st, blocks, D, (const float*)pb, dbeta, accumulate);
+  return nl_check_launch("nl_layernorm_bwd");
+}
+
+extern "C" size_t nl_colsum_ws_bytes(int rows, int cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  return (size_t)((rows + kColsumRows - 1) / kColsumRows) * cols * sizeof(float);
+}
+
+extern "C" int nl_colsum_bf16(void* stream, int rows, int cols, const nl_bf16* x, int64_t ld, float* out,
+                              int accumulate, void* ws, size_t ws_bytes) {
+  if (rows <= 0 || cols <= 0) return nl_set_error(NL_EINVAL, "colsum: need rows > 0 and cols > 0");
+  if (ld < cols) return nl_set_error(NL_EINVAL, "colsum: ld < cols");
+  if (!x || !out || !ws) return nl_set_error(NL_EINVAL, "colsum: null pointer");
+  if ((((uintptr_t)x | (uintptr_t)ws) & 15) != 0 || (ld & 7) != 0)
+    return nl_set_error(NL_EALIGN, "colsum: x and ws must be 16-byte aligned and ld % 8 == 0");
+  if (ws_bytes < nl_colsum_ws_bytes(rows, cols))
+    return nl_set_error(NL_EINVAL, "colsum: workspace smaller than nl_colsum_ws_bytes()");
+  const int P = (rows + kColsumRows - 1) / kColsumRows;
+  if (P > 65535) return nl_set_error(NL_EINVAL, "colsum: too many rows");
+  float* part = static_cast<float*>(ws);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(colsum_partial_kernel, dim3((cols + 511) / 512, P), dim3(256), 0, st, rows, cols, x, ld, part);
+  hipLaunchKernelGGL(sum_partials_kernel, dim3((cols + 63) / 64), dim3(1024), 0, st, P, cols, (const float*)part, out,
+                     accumulate);
+  return nl_check_launch("nl_colsum_bf16");
+}
+
+extern "C" int nl_embedding_fwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
+                                const float* tok, const float* pos, nl_bf16* out) {
+  if (batch < 0 || seq < 0 || D <= 0 || (D % 4) != 0 || vocab <= 0)
+    return nl_set_error(NL_EINVAL, "embedding: need D % 4 == 0 and vocab > 0");
+  if (batch == 0 || seq == 0) return NL_OK;
+  if (!ids || !tok || !pos || !out) return nl_set_error(NL_EINVAL, "embedding: null pointer");
+  if ((((uintptr_t)tok | (uintptr_t)pos) & 15) != 0 || ((uintptr_t)out & 7) != 0)
+    return nl_set_error(NL_EALIGN, "embedding: tables must be 16-byte and out 8-byte aligned");
+  if ((int64_t)batch * seq > 0x7fffffff) return nl_set_error(NL_EINVAL, "embedding: too many tokens");
+  hipLaunchKernelGGL(embed_fwd_kernel, dim3(batch * seq), dim3(128), 0, (hipStream_t)stream, seq, D, ids, tok, pos,
+                     out, vocab);
+  return nl_check_launch("nl_embedding_fwd");
+}
+
+extern "C" int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
+                                const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos) {
+  if (batch < 0 || seq < 0 || D <= 0 || vocab <= 0) return nl_set_error(NL_EINVAL, "embedding_bwd: bad shape");
+  if (batch == 0 || seq == 0) return NL_OK;
+  if (!ids || !dx || !dtok || !dpos) return nl_set_error(NL_EINVAL, "embedding_bwd: null pointer");
+  if ((int64_t)batch * seq > 0x7fffffff) return nl_set_error(NL_EINVAL, "embedding_bwd: too many tokens");
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(embed_bwd_tok_kernel, dim3(batch * seq), dim3(128), 0, st, D, ids, dx, dtok, vocab);
+  hipLaunchKernelGGL(embed_bwd_pos_kernel, dim3(seq), dim3(128), 0, st, batch, seq, D, dx, dpos, accumulate_pos);
+  return nl_check_launch("nl_embedding_bwd");
+}

@@ -54,6 +54,11 @@ struct GemmArgs {
   int k_chunk;
   float* ws;      // fp32 partials [split][M][ldw] when splitting, else null
   int64_t ldw;
+  // fused epilogue (NL_EPI_*): bias[N] fp32, aux [M][ldaux] bf16
+  int epi;
+  const float* bias;
+  uint16_t* aux;
+  int64_t ldaux;
 };
 
 __device__ __forceinline__ int swz(int row, int kc) { return (kc ^ ((row ^ (row >> 3)) & 7)); }
@@ -174,6 +179,93 @@ template <>
 __device__ __forceinline__ void store1<float>(float* c, float v) { *c = v; }
 template <>
 __device__ __forceinline__ void store1<uint16_t>(uint16_t* c, float v) { *c = f32_to_bf16(v); }
+
+// Output of one lane's 4 consecutive columns C[m][n..n+3] (v = alpha * s * acc):
+//   NL_EPI_BIAS       v += b[0..3]                          (then + beta * C)
+//   NL_EPI_BIAS_GELU  u = bf16(v + b[0..3]); aux = u; C = gelu(u)
+//   NL_EPI_DGELU      C = v * gelu'(a[0..3])                (a = the saved u)
+// b = bias[n..n+3], a = aux[m][n..n+3], already fetched by the caller (entries
+// at or beyond N are unspecified). Columns at or beyond N are not written.
+template <typename OutT, int EPI>
+__device__ __forceinline__ void epilogue_apply(const GemmArgs& g, int64_t m, int n, float v[4], const f32x4& b,
+                                               const u32x2& a) {
+  OutT* crow = reinterpret_cast<OutT*>(g.C) + m * g.ldc;
+  const bool full = n + 4 <= g.N;
+  if constexpr (EPI == NL_EPI_BIAS || EPI == NL_EPI_BIAS_GELU) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += b[e];
+  }
+  if constexpr (EPI == NL_EPI_BIAS_GELU) {
+    uint16_t* arow = g.aux + m * g.ldaux;
+    uint16_t u[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      u[e] = f32_to_bf16(v[e]);
+      v[e] = gelu_tanh(bf16_to_f32(u[e]));
+    }
+    if (full) {
+      *reinterpret_cast<u32x2*>(arow + n) =
+          u32x2{(uint32_t)u[0] | ((uint32_t)u[1] << 16), (uint32_t)u[2] | ((uint32_t)u[3] << 16)};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (n + e < g.N) arow[n + e] = u[e];
+    }
+  } else if constexpr (EPI == NL_EPI_DGELU) {
+    v[0] *= gelu_tanh_grad(bf16_lo(a[0]));
+    v[1] *= gelu_tanh_grad(bf16_hi(a[0]));
+    v[2] *= gelu_tanh_grad(bf16_lo(a[1]));
+    v[3] *= gelu_tanh_grad(bf16_hi(a[1]));
+  }
+  // the GELU forms are validated to have beta == 0
+  const bool use_beta = (EPI == NL_EPI_NONE || EPI == NL_EPI_BIAS) && g.beta != 0.f;
+  if (full) {
+    if (use_beta) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += g.beta * load1(crow + n + e);
+    }
+    store4(crow + n, v[0], v[1], v[2], v[3]);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (n + e < g.N) {
+        float x = v[e];
+        if (use_beta) x += g.beta * load1(crow + n + e);
+        store1(crow + n + e, x);
+      }
+    }
+  }
+}
+
+// Epilogue with its operands fetched from global memory, dispatching on g.epi
+// (the split-K reduction and the register-staged kernel).
+template <typename OutT>
+__device__ __forceinline__ void epilogue4_any(const GemmArgs& g, int64_t m, int n, float v[4]) {
+  const bool full = n + 4 <= g.N;
+  f32x4 b = {0.f, 0.f, 0.f, 0.f};
+  u32x2 a = {0u, 0u};
+  if (g.epi == NL_EPI_BIAS || g.epi == NL_EPI_BIAS_GELU) {
+    if (full) b = *reinterpret_cast<const f32x4*>(g.bias + n);
+    else
+      for (int e = 0; e < 4; ++e) b[e] = n + e < g.N ? g.bias[n + e] : 0.f;
+  }
+  if (g.epi == NL_EPI_DGELU) {
+    const uint16_t* arow = g.aux + m * g.ldaux;
+    if (full) a = *reinterpret_cast<const u32x2*>(arow + n);
+    else {
+      uint16_t t[4] = {0, 0, 0, 0};
+      for (int e = 0; e < 4; ++e)
+        if (n + e < g.N) t[e] = arow[n + e];
+      a = u32x2{(uint32_t)t[0] | ((uint32_t)t[1] << 16), (uint32_t)t[2] | ((uint32_t)t[3] << 16)};
+    }
+  }
+  switch (g.epi) {
+    case NL_EPI_BIAS: epilogue_apply<OutT, NL_EPI_BIAS>(g, m, n, v, b, a); break;
+    case NL_EPI_BIAS_GELU: epilogue_apply<OutT, NL_EPI_BIAS_GELU>(g, m, n, v, b, a); break;
+    case NL_EPI_DGELU: epilogue_apply<OutT, NL_EPI_DGELU>(g, m, n, v, b, a); break;
+    default: epilogue_apply<OutT, NL_EPI_NONE>(g, m, n, v, b, a); break;
+  }
+}
 
 template <int BM, int BN, int WM, int WN, bool A_KMAJ, bool B_KMAJ, typename OutT>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
@@ -321,38 +413,19 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   // epilogue: lane holds C[m][n..n+3] for m = row of lane, n = 8q + 4*(lane/32)
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
-  OutT* C = reinterpret_cast<OutT*>(g.C);
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int m = m0 + wm * WTM + i * 32 + frow;
     if (m >= g.M) continue;
-    OutT* crow = C + (int64_t)m * g.ldc;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
-        float v0 = acc[i][j][4 * q + 0] * s, v1 = acc[i][j][4 * q + 1] * s;
-        float v2 = acc[i][j][4 * q + 2] * s, v3 = acc[i][j][4 * q + 3] * s;
-        if (n + 4 <= g.N) {
-          if (g.beta != 0.f) {
-            v0 += g.beta * load1(crow + n + 0);
-            v1 += g.beta * load1(crow + n + 1);
-            v2 += g.beta * load1(crow + n + 2);
-            v3 += g.beta * load1(crow + n + 3);
-          }
-          store4(crow + n, v0, v1, v2, v3);
-        } else {
-          const float vv[4] = {v0, v1, v2, v3};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (n + e < g.N) {
-              float v = vv[e];
-              if (g.beta != 0.f) v += g.beta * load1(crow + n + e);
-              store1(crow + n + e, v);
-            }
-          }
-        }
+        if (n >= g.N) continue;
+        float v[4] = {acc[i][j][4 * q + 0] * s, acc[i][j][4 * q + 1] * s, acc[i][j][4 * q + 2] * s,
+                      acc[i][j][4 * q + 3] * s};
+        epilogue4_any<OutT>(g, m, n, v);
       }
     }
   }
@@ -506,7 +579,7 @@ __device__ __forceinline__ void wait_stage(int later) {
   }
 }
 
-template <int BM, int BN, int BKT, int S, bool A_KMAJ, bool B_KMAJ, typename OutT>
+template <int BM, int BN, int BKT, int S, bool A_KMAJ, bool B_KMAJ, typename OutT, int EPI>
 __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   constexpr int NT = 256;
   constexpr int WTM = BM / 2, WTN = BN / 2;
@@ -642,68 +715,89 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
     }
     return;
   }
+  // Epilogue operands (bias columns, the saved pre-activation tile) are staged
+  // into LDS by DMA before the first store: a wait on a vector load also waits
+  // for every earlier store, so loads mixed into the store stream would
+  // serialise it. The operand tiles' LDS is free once all waves pass the barrier.
+  constexpr bool kBias = EPI == NL_EPI_BIAS || EPI == NL_EPI_BIAS_GELU;
+  constexpr bool kAux = EPI == NL_EPI_DGELU;
+  static_assert(!kAux || S * STAGE * 2 >= BM * BN * 2, "aux tile must fit the pipeline LDS");
+  static_assert(BN == 128, "the staged epilogue assumes 128-column tiles");
+  const float* sbias = reinterpret_cast<const float*>(smem);
+  if constexpr (kBias || kAux) {
+    __syncthreads();
+    if constexpr (kBias) {
+      // bias[n0 .. n0+255] -> 1 KB (only the first 128 are read); clipped at N
+      if (wave == 0) {
+        const __amdgpu_buffer_rsrc_t rbias = make_rsrc(g.bias, (uint32_t)g.N * 4u);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rbias, (lds_void*)smem, 16, (uint32_t)(n0 + lane * 4) * 4u, 0, 0, 0);
+      }
+    } else {
+      // aux tile [128][128] bf16: row r at r*256 bytes, 16-byte chunk c at slot c ^ (r & 15)
+      const uint32_t aux_bytes = (uint32_t)(((int64_t)g.M * g.ldaux) * 2);
+      const __amdgpu_buffer_rsrc_t raux = make_rsrc(g.aux, aux_bytes);
+#pragma unroll
+      for (int i = 0; i < BM * BN * 2 / 1024 / kNW; ++i) {
+        const int blk = i * kNW + wave;            // 1 KB block = 4 rows
+        const int r = blk * 4 + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        const uint32_t off = (uint32_t)(((int64_t)(m0 + r) * g.ldaux + n0 + c * 8) * 2);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(raux, (lds_void*)(smem + blk * 512), 16, off, 0, 0, 0);
+      }
+    }
+    wait_vm<0>();
+    __syncthreads();
+  }
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
-  OutT* C = reinterpret_cast<OutT*>(g.C);
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WTM + i * 32 + frow;
+    const int ml = wm * WTM + i * 32 + frow;
+    const int m = m0 + ml;
     if (m >= g.M) continue;
-    OutT* crow = C + (int64_t)m * g.ldc;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
-        float v0 = acc[i][j][4 * q + 0] * s, v1 = acc[i][j][4 * q + 1] * s;
-        float v2 = acc[i][j][4 * q + 2] * s, v3 = acc[i][j][4 * q + 3] * s;
-        if (n + 4 <= g.N) {
-          if (g.beta != 0.f) {
-            v0 += g.beta * load1(crow + n + 0);
-            v1 += g.beta * load1(crow + n + 1);
-            v2 += g.beta * load1(crow + n + 2);
-            v3 += g.beta * load1(crow + n + 3);
-          }
-          store4(crow + n, v0, v1, v2, v3);
-        } else {
-          const float vv[4] = {v0, v1, v2, v3};
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if (n + e < g.N) {
-              float v = vv[e];
-              if (g.beta != 0.f) v += g.beta * load1(crow + n + e);
-              store1(crow + n + e, v);
-            }
-          }
-        }
+        const int nl = wn * WTN + j * 32 + q * 8 + g4;
+        const int n = n0 + nl;
+        if (n >= g.N) continue;
+        float v[4] = {acc[i][j][4 * q + 0] * s, acc[i][j][4 * q + 1] * s, acc[i][j][4 * q + 2] * s,
+                      acc[i][j][4 * q + 3] * s};
+        f32x4 b = {0.f, 0.f, 0.f, 0.f};
+        u32x2 a = {0u, 0u};
+        if constexpr (kBias) b = *reinterpret_cast<const f32x4*>(sbias + nl);
+        if constexpr (kAux)
+          a = *reinterpret_cast<const u32x2*>(smem + ml * 128 + (((nl >> 3) ^ (ml & 15)) << 3) + (nl & 7));
+        epilogue_apply<OutT, EPI>(g, m, n, v, b, a);
       }
     }
   }
 }
 
-// Explicit instantiations: every (tile, pipeline, layout, output) combination
-// the dispatcher can launch gets its host stub emitted.
-#define NL_I(BM, BKT, S, AK, BKM, T) template __global__ void gemm2_kernel<BM, BM, BKT, S, AK, BKM, T>(GemmArgs);
-#define NL_I4(BM, BKT, S, T)                                                                 \
-  NL_I(BM, BKT, S, true, false, T) NL_I(BM, BKT, S, true, true, T) NL_I(BM, BKT, S, false, false, T) \
-  NL_I(BM, BKT, S, false, true, T)
-#define NL_I8(BM, BKT, S) NL_I4(BM, BKT, S, float) NL_I4(BM, BKT, S, uint16_t)
-NL_I8(128, 64, 2)
-NL_I8(128, 32, 2)
+// Explicit instantiations: every (layout, output, epilogue) combination the
+// dispatcher can launch gets its host stub emitted. k-stage depth per layout:
+// 64 when both operands are k-major (NT), else 32 (see launch_cfg).
+#define NL_I(AK, BKM, T, E) template __global__ void gemm2_kernel<128, 128, (AK && BKM) ? 64 : 32, 2, AK, BKM, T, E>(GemmArgs);
+#define NL_I4(T, E) NL_I(true, false, T, E) NL_I(true, true, T, E) NL_I(false, false, T, E) NL_I(false, true, T, E)
+#define NL_I8(E) NL_I4(float, E) NL_I4(uint16_t, E)
+NL_I8(NL_EPI_NONE)
+NL_I8(NL_EPI_BIAS)
+NL_I8(NL_EPI_BIAS_GELU)
+NL_I8(NL_EPI_DGELU)
 #undef NL_I8
 #undef NL_I4
 #undef NL_I
 
 // beta*C for the degenerate K == 0 case is handled by the main kernel (nk = 0).
 
-// C = alpha * s * sum_split ws[split] + beta * C, summed in split order (deterministic).
+// C = epilogue(alpha * s * sum_split ws[split]), summed in split order (deterministic).
 template <typename OutT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int splits) {
   const int64_t groups_n = (g.N + 3) / 4;
   const int64_t total = (int64_t)g.M * groups_n;
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
-  OutT* C = reinterpret_cast<OutT*>(g.C);
   const int64_t plane = (int64_t)g.M * g.ldw;
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t m = i / groups_n;
@@ -717,19 +811,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int spli
       acc[2] += p[2];
       acc[3] += p[3];
     }
-    OutT* crow = C + m * g.ldc;
-    if (n + 4 <= g.N) {
-      float v[4] = {acc[0] * s, acc[1] * s, acc[2] * s, acc[3] * s};
-      if (g.beta != 0.f)
-        for (int e = 0; e < 4; ++e) v[e] += g.beta * load1(crow + n + e);
-      store4(crow + n, v[0], v[1], v[2], v[3]);
-    } else {
-      for (int e = 0; e < 4 && n + e < g.N; ++e) {
-        float v = acc[e] * s;
-        if (g.beta != 0.f) v += g.beta * load1(crow + n + e);
-        store1(crow + n + e, v);
-      }
-    }
+    float v[4] = {acc[0] * s, acc[1] * s, acc[2] * s, acc[3] * s};
+    epilogue4_any<OutT>(g, m, n, v);
   }
 }
 
@@ -779,13 +862,32 @@ void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
   // the v2 kernel addresses operands with 32-bit buffer offsets
   const int64_t a_ext = (AK ? (int64_t)g.M + BM : (int64_t)g.K + BK) * g.lda * 2;
   const int64_t b_ext = (BK_ ? (int64_t)g.N + BN : (int64_t)g.K + BK) * g.ldb * 2;
-  const bool v2 = WM == 2 && WN == 2 && a_ext < ((int64_t)1 << 31) && b_ext < ((int64_t)1 << 31);
+  // (the DGELU epilogue also reads its aux tile through a buffer descriptor)
+  const int64_t aux_ext = g.epi == NL_EPI_DGELU ? ((int64_t)g.M + BM) * g.ldaux * 2 : 0;
+  const bool v2 = WM == 2 && WN == 2 && a_ext < ((int64_t)1 << 31) && b_ext < ((int64_t)1 << 31) &&
+                  aux_ext < ((int64_t)1 << 31);
   // Pipeline choice measured on MI355X at the model's shapes: with both
   // operands k-major (NT) 64-k stages win; otherwise 32-k stages (32 KB of LDS,
   // more workgroups per CU to cover L2-miss latency) win.
   auto launch2 = [&](int grid) {
-    if (AK && BK_) hipLaunchKernelGGL((gemm2_kernel<128, 128, 64, 2, AK, BK_, OutT>), dim3(grid), dim3(256), 0, st, g);
-    else hipLaunchKernelGGL((gemm2_kernel<128, 128, 32, 2, AK, BK_, OutT>), dim3(grid), dim3(256), 0, st, g);
+    constexpr int BKT = (AK && BK_) ? 64 : 32;
+    // with split K the epilogue runs in the reduction kernel
+    const int epi = g.ws ? NL_EPI_NONE : g.epi;
+    switch (epi) {
+      case NL_EPI_BIAS:
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_BIAS>), dim3(grid), dim3(256), 0, st, g);
+        break;
+      case NL_EPI_BIAS_GELU:
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_BIAS_GELU>), dim3(grid), dim3(256), 0,
+                           st, g);
+        break;
+      case NL_EPI_DGELU:
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_DGELU>), dim3(grid), dim3(256), 0, st,
+                           g);
+        break;
+      default:
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(256), 0, st, g);
+    }
   };
   if (p.splits > 1) {
     g.ldw = p.ldw;  // g.ws already set by the caller
@@ -830,9 +932,10 @@ extern "C" size_t nl_gemm_ws_bytes(int opA, int opB, int M, int N, int K) {
   return make_plan(M, N, K).ws_bytes;
 }
 
-extern "C" int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
-                          int64_t lda, const nl_bf16* B, int64_t ldb, float beta, void* C, int c_dtype, int64_t ldc,
-                          const float* alpha_dev, void* ws, size_t ws_bytes) {
+extern "C" int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
+                             int64_t lda, const nl_bf16* B, int64_t ldb, float beta, void* C, int c_dtype, int64_t ldc,
+                             const float* alpha_dev, int epi, const float* bias, nl_bf16* aux, int64_t ldaux, void* ws,
+                             size_t ws_bytes) {
   if (opA != NL_OP_N && opA != NL_OP_T) return nl_set_error(NL_EINVAL, "gemm: opA must be NL_OP_N or NL_OP_T");
   if (opB != NL_OP_N && opB != NL_OP_T) return nl_set_error(NL_EINVAL, "gemm: opB must be NL_OP_N or NL_OP_T");
   if (c_dtype != NL_DTYPE_F32 && c_dtype != NL_DTYPE_BF16) return nl_set_error(NL_EINVAL, "gemm: bad c_dtype");
@@ -848,6 +951,14 @@ extern "C" int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K, f
     return nl_set_error(NL_EALIGN, "gemm: A, B and C must be 16-byte aligned");
   if (((lda | ldb | ldc) & 7) != 0) return nl_set_error(NL_EALIGN, "gemm: lda, ldb, ldc must be multiples of 8");
   if ((int64_t)M * N > ((int64_t)1 << 40)) return nl_set_error(NL_EINVAL, "gemm: output too large");
+  if (epi < NL_EPI_NONE || epi > NL_EPI_DGELU) return nl_set_error(NL_EINVAL, "gemm: unknown epilogue");
+  if ((epi == NL_EPI_BIAS || epi == NL_EPI_BIAS_GELU) && (!bias || ((uintptr_t)bias & 15) != 0))
+    return nl_set_error(NL_EINVAL, "gemm: bias epilogue needs a 16-byte aligned fp32 bias[N]");
+  if (epi == NL_EPI_BIAS_GELU || epi == NL_EPI_DGELU) {
+    if (!aux || ((uintptr_t)aux & 15) != 0 || ldaux < N || (ldaux & 7) != 0)
+      return nl_set_error(NL_EINVAL, "gemm: GELU epilogue needs a 16-byte aligned bf16 aux with ldaux >= N, ldaux % 8 == 0");
+    if (beta != 0.f) return nl_set_error(NL_EINVAL, "gemm: GELU epilogues need beta == 0");
+  }
 
   GemmArgs g;
   g.M = M;
@@ -862,6 +973,10 @@ extern "C" int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K, f
   g.alpha = alpha;
   g.beta = beta;
   g.alpha_dev = alpha_dev;
+  g.epi = epi;
+  g.bias = bias;
+  g.aux = aux;
+  g.ldaux = ldaux;
   Plan p = make_plan(M, N, K);
   if (p.splits > 1 && (!ws || ws_bytes < p.ws_bytes || ((uintptr_t)ws & 15) != 0)) {
     // no (usable) workspace: one workgroup per tile over the whole K range
@@ -874,6 +989,13 @@ extern "C" int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K, f
   if (c_dtype == NL_DTYPE_F32) launch_typed<float>(opA, opB, g, p, st);
   else launch_typed<uint16_t>(opA, opB, g, p, st);
   return nl_check_launch("nl_gemm");
+}
+
+extern "C" int nl_gemm_ex(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
+                          int64_t lda, const nl_bf16* B, int64_t ldb, float beta, void* C, int c_dtype, int64_t ldc,
+                          const float* alpha_dev, void* ws, size_t ws_bytes) {
+  return nl_gemm_fused(stream, opA, opB, M, N, K, alpha, A, lda, B, ldb, beta, C, c_dtype, ldc, alpha_dev,
+                       NL_EPI_NONE, nullptr, nullptr, 0, ws, ws_bytes);
 }
 
 extern "C" int nl_gemm(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,

@@ -1,0 +1,229 @@
+"""nlearn_amd.kernels.fused — the model's non-GEMM layers on the HIP kernels.
+
+* ``layer_norm(x, gamma, beta)`` and ``add_layer_norm(x, r, gamma, beta)``:
+  LayerNorm with fp32 statistics (nlearn/model.py:228-241), the second one
+  with the residual add of the block folded in (model.py:315-324): it returns
+  both LN(x + r) and the new residual stream x + r, reading x and r once.
+* ``ffn(x, W1, b1, W2, b2)``: the FFN (model.py:266-277, with the benchmark's
+  tanh-GELU and biases) as two GEMMs whose epilogues add the biases and apply
+  the GELU; the backward's dX GEMM applies the GELU derivative in its
+  epilogue, so no elementwise kernel runs between the GEMMs.
+* ``embedding(ids, tok, pos)``: token + learned-position lookup (model.py:75-85).
+
+Every op is an autograd Function whose forward and backward are C-ABI calls;
+there is no framework fallback.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from .gemm import (EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU, _check_device, _kernel_ready, _ld, bf16_shadow, gemm_raw,
+                   padded_empty)
+
+_BF16 = torch.bfloat16
+_F32 = torch.float32
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    """Dense bf16 [rows, D] view of x (copies only if x is not already one)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.dtype != _BF16:
+        x2 = x2.to(_BF16)
+    if not x2.is_contiguous() or x2.data_ptr() % 16:
+        x2 = x2.contiguous()
+    return x2
+
+
+def _param(p: torch.Tensor) -> torch.Tensor:
+    p = p.detach()
+    if p.dtype != _F32:
+        p = p.to(_F32)
+    return p.contiguous()
+
+
+# ---------------------------------------------------------------------------
+# LayerNorm
+# ---------------------------------------------------------------------------
+
+
+def layer_norm_fwd_raw(x2, gamma, beta, eps, residual=None):
+    """-> y, s, mean, rstd with s = bf16(x + residual) (None without a residual)."""
+    _check_device(x2, gamma, beta)
+    rows, D = x2.shape
+    y = torch.empty_like(x2)
+    s = torch.empty_like(x2) if residual is not None else None
+    mean = torch.empty(rows, dtype=_F32, device=x2.device)
+    rstd = torch.empty(rows, dtype=_F32, device=x2.device)
+    _lib.call("nl_layernorm_fwd", _stream(x2), rows, D, x2.data_ptr(),
+              residual.data_ptr() if residual is not None else None, s.data_ptr() if s is not None else None,
+              gamma.data_ptr(), beta.data_ptr(), float(eps), y.data_ptr(), mean.data_ptr(), rstd.data_ptr())
+    return y, s, mean, rstd
+
+
+def layer_norm_bwd_raw(dy2, xin, mean, rstd, gamma, dres=None):
+    """-> dx (+ dres), dgamma, dbeta."""
+    rows, D = dy2.shape
+    dx = torch.empty_like(dy2)
+    dgamma = torch.empty(D, dtype=_F32, device=dy2.device)
+    dbeta = torch.empty(D, dtype=_F32, device=dy2.device)
+    wsb = int(_lib.load().nl_layernorm_bwd_ws_bytes(rows, D))
+    ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=dy2.device)
+    _lib.call("nl_layernorm_bwd", _stream(dy2), rows, D, dy2.data_ptr(), xin.data_ptr(), mean.data_ptr(),
+              rstd.data_ptr(), gamma.data_ptr(), dres.data_ptr() if dres is not None else None, dx.data_ptr(),
+              dgamma.data_ptr(), dbeta.data_ptr(), 0, ws.data_ptr(), wsb)
+    return dx, dgamma, dbeta
+
+
+class _LayerNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, gamma, beta, eps):
+        x2 = _rows(x)
+        g, b = _param(gamma), _param(beta)
+        y, _, mean, rstd = layer_norm_fwd_raw(x2, g, b, eps)
+        ctx.save_for_backward(x2, mean, rstd, g)
+        ctx.shape = x.shape
+        return y.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, mean, rstd, g = ctx.saved_tensors
+        dx, dg, db = layer_norm_bwd_raw(_rows(dy), x2, mean, rstd, g)
+        return dx.view(ctx.shape), dg, db, None
+
+
+class _AddLayerNorm(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, r, gamma, beta, eps):
+        ctx.set_materialize_grads(False)
+        x2, r2 = _rows(x), _rows(r)
+        if x2.shape != r2.shape:
+            raise ValueError("add_layer_norm: x and r differ in shape")
+        g, b = _param(gamma), _param(beta)
+        y, s, mean, rstd = layer_norm_fwd_raw(x2, g, b, eps, residual=r2)
+        ctx.save_for_backward(s, mean, rstd, g)
+        ctx.shape = x.shape
+        return y.view(x.shape), s.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy, ds):
+        s, mean, rstd, g = ctx.saved_tensors
+        if dy is None:
+            dx = _rows(ds)
+            return dx.view(ctx.shape), dx.view(ctx.shape), None, None, None
+        dx, dg, db = layer_norm_bwd_raw(_rows(dy), s, mean, rstd, g, dres=_rows(ds) if ds is not None else None)
+        dx = dx.view(ctx.shape)
+        return dx, dx, dg, db, None
+
+
+def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """bf16 LayerNorm over the last dimension, fp32 statistics and parameters."""
+    return _LayerNorm.apply(x, gamma, beta, eps)
+
+
+def add_layer_norm(x: torch.Tensor, r: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor,
+                   eps: float = 1e-5):
+    """(LN(s), s) with s = bf16(x + r): the residual add and the next LayerNorm in one pass."""
+    return _AddLayerNorm.apply(x, r, gamma, beta, eps)
+
+
+# ---------------------------------------------------------------------------
+# bias gradients
+# ---------------------------------------------------------------------------
+
+
+def colsum(x2: torch.Tensor) -> torch.Tensor:
+    """fp32 column sums of a bf16 [rows, cols] matrix (fixed summation order)."""
+    rows, cols = x2.shape
+    x2 = _kernel_ready(x2)
+    out = torch.empty(cols, dtype=_F32, device=x2.device)
+    wsb = int(_lib.load().nl_colsum_ws_bytes(rows, cols))
+    ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=x2.device)
+    _lib.call("nl_colsum_bf16", _stream(x2), rows, cols, x2.data_ptr(), _ld(x2), out.data_ptr(), 0, ws.data_ptr(),
+              wsb)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# FFN
+# ---------------------------------------------------------------------------
+
+
+class _FFN(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, W1, b1, W2, b2):
+        x2 = _rows(x)
+        W1b, W2b = bf16_shadow(W1), bf16_shadow(W2)
+        b1f, b2f = _param(b1), _param(b2)
+        M, F_ = x2.shape[0], W1b.shape[1]
+        u = padded_empty(M, F_, _BF16, x2.device)         # pre-activation, kept for the backward
+        h = padded_empty(M, F_, _BF16, x2.device)         # gelu(u)
+        gemm_raw(x2, W1b, out=h, epi=EPI_BIAS_GELU, bias=b1f, aux=u)
+        y = padded_empty(M, W2b.shape[1], _BF16, x2.device)
+        gemm_raw(h, W2b, out=y, epi=EPI_BIAS, bias=b2f)
+        ctx.save_for_backward(x2, u, h, W1, W2)
+        ctx.wb = (W1b, W2b)
+        ctx.shape = x.shape
+        return y.view(*x.shape[:-1], W2b.shape[1])
+
+    @staticmethod
+    def backward(ctx, dy):
+        x2, u, h, W1, W2 = ctx.saved_tensors
+        W1b, W2b = ctx.wb
+        dy2 = _rows(dy)
+        db2 = colsum(dy2)
+        dW2 = gemm_raw(h, dy2, "T", "N", out_dtype=_F32)                          # h^T . dy
+        du = padded_empty(u.shape[0], u.shape[1], _BF16, dy2.device)
+        gemm_raw(dy2, W2b, "N", "T", out=du, epi=EPI_DGELU, aux=u)               # (dy . W2^T) * gelu'(u)
+        db1 = colsum(du)
+        dW1 = gemm_raw(x2, du, "T", "N", out_dtype=_F32)                          # x^T . du
+        dx = gemm_raw(du, W1b, "N", "T", out_dtype=_BF16)                          # du . W1^T
+        return dx.view(ctx.shape), dW1, db1, dW2, db2
+
+
+def ffn(x: torch.Tensor, W1: torch.Tensor, b1: torch.Tensor, W2: torch.Tensor, b2: torch.Tensor) -> torch.Tensor:
+    """gelu_tanh(x @ W1 + b1) @ W2 + b2 in bf16 with fp32 accumulation."""
+    return _FFN.apply(x, W1, b1, W2, b2)
+
+
+# ---------------------------------------------------------------------------
+# embedding
+# ---------------------------------------------------------------------------
+
+
+class _Embedding(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, ids, tok, pos):
+        B, S = ids.shape
+        V, D = tok.shape
+        if S > pos.shape[0]:
+            raise ValueError(f"embedding: sequence {S} exceeds the position table ({pos.shape[0]})")
+        ids32 = ids.to(torch.int32).contiguous()
+        t, p = _param(tok), _param(pos)
+        _check_device(ids32, t, p)
+        out = torch.empty((B, S, D), dtype=_BF16, device=ids.device)
+        _lib.call("nl_embedding_fwd", _stream(out), B, S, D, V, ids32.data_ptr(), t.data_ptr(), p.data_ptr(),
+                  out.data_ptr())
+        ctx.save_for_backward(ids32)
+        ctx.dims = (B, S, D, V, tuple(pos.shape))
+        return out
+
+    @staticmethod
+    def backward(ctx, dx):
+        (ids32,) = ctx.saved_tensors
+        B, S, D, V, pshape = ctx.dims
+        dx = dx.to(_BF16).contiguous()
+        dtok = torch.zeros((V, D), dtype=_F32, device=dx.device)
+        dpos = torch.zeros(pshape, dtype=_F32, device=dx.device)
+        _lib.call("nl_embedding_bwd", _stream(dx), B, S, D, V, ids32.data_ptr(), dx.data_ptr(), dtok.data_ptr(),
+                  dpos.data_ptr(), 0)
+        return None, dtok, dpos
+
+
+def embedding(ids: torch.Tensor, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+    """bf16 (B, S, D) = tok[ids] + pos[:S] for int ids (B, S)."""
+    return _Embedding.apply(ids, tok, pos)

@@ -67,12 +67,18 @@ def padded_empty(rows: int, cols: int, dtype=_BF16, device="cuda") -> torch.Tens
     return torch.empty((rows, ld), dtype=dtype, device=device)[:, :cols]
 
 
+EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU = 0, 1, 2, 3
+
+
 def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", out_dtype=_F32,
              out: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 0.0,
-             alpha_dev: torch.Tensor | None = None) -> torch.Tensor:
-    """C = alpha * [*alpha_dev] * op(A) @ op(B) + beta * C on the current stream.
+             alpha_dev: torch.Tensor | None = None, epi: int = EPI_NONE, bias: torch.Tensor | None = None,
+             aux: torch.Tensor | None = None) -> torch.Tensor:
+    """C = epilogue(alpha * [*alpha_dev] * op(A) @ op(B)) on the current stream.
 
     opA == "T": A is stored [K, M]; opB == "T": B is stored [N, K].
+    epi: EPI_NONE (+ beta * C), EPI_BIAS (+ bias[N] + beta * C), EPI_BIAS_GELU
+    (aux = bf16(v + bias), C = gelu_tanh(aux)), EPI_DGELU (C = v * gelu_tanh'(aux)).
     """
     _check_device(A, B)
     A = _kernel_ready(A)
@@ -93,15 +99,23 @@ def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", o
         raise ValueError(f"gemm: output shape {tuple(out.shape)} != {(M, N)}")
     if alpha_dev is not None and (alpha_dev.dtype != _F32 or not alpha_dev.is_cuda):
         raise ValueError("gemm: alpha_dev must be a float32 device scalar")
+    if epi in (EPI_BIAS, EPI_BIAS_GELU):
+        if bias is None or bias.dtype != _F32 or bias.numel() != N or not bias.is_contiguous():
+            raise ValueError("gemm: the bias epilogue needs a contiguous float32 bias of N elements")
+    if epi in (EPI_BIAS_GELU, EPI_DGELU):
+        if aux is None or aux.dtype != _BF16 or tuple(aux.shape) != (M, N):
+            raise ValueError(f"gemm: the GELU epilogues need a bf16 aux of shape {(M, N)}")
     stream = torch.cuda.current_stream(A.device).cuda_stream
     oa = _lib.NL_OP_T if opA == "T" else _lib.NL_OP_N
     ob = _lib.NL_OP_T if opB == "T" else _lib.NL_OP_N
     wsb = int(_lib.load().nl_gemm_ws_bytes(oa, ob, M, N, K))
     ws = torch.empty(wsb // 4, dtype=_F32, device=A.device) if wsb else None
-    _lib.call("nl_gemm_ex", stream, oa, ob, M, N, K, float(alpha),
+    _lib.call("nl_gemm_fused", stream, oa, ob, M, N, K, float(alpha),
               A.data_ptr(), _ld(A), B.data_ptr(), _ld(B), float(beta), out.data_ptr(),
               _lib.NL_DTYPE_F32 if out.dtype == _F32 else _lib.NL_DTYPE_BF16, _ld(out),
-              alpha_dev.data_ptr() if alpha_dev is not None else None,
+              alpha_dev.data_ptr() if alpha_dev is not None else None, int(epi),
+              bias.data_ptr() if bias is not None else None,
+              aux.data_ptr() if aux is not None else None, _ld(aux) if aux is not None else 0,
               ws.data_ptr() if ws is not None else None, wsb)
     return out
 

@@ -22,9 +22,9 @@ from dataclasses import dataclass
 
 import numpy as np
 import torch
-import torch.nn.functional as F
 
 from .attention import flash_attention_qkv
+from .kernels import fused
 from .kernels.gemm import linear
 
 COMPUTE_DTYPE = torch.bfloat16
@@ -126,16 +126,14 @@ def count_params(params) -> int:
 
 
 def embed(params, token_ids: torch.Tensor) -> torch.Tensor:
-    """token + learned position embeddings -> bf16 (bs, seq, d)."""
-    S = token_ids.shape[-1]
+    """token + learned position embeddings -> bf16 (bs, seq, d) (one HIP kernel)."""
     e = params["embeddings"]
-    x = F.embedding(token_ids.long(), e["token_embed"]) + e["pos_embed"][:S]
-    return x.to(COMPUTE_DTYPE)
+    return fused.embedding(token_ids, e["token_embed"], e["pos_embed"])
 
 
 def layer_norm(p, x: torch.Tensor, eps: float = BASELINE.ln_eps) -> torch.Tensor:
-    """Pre-LN LayerNorm with learned gamma / beta, in x's dtype (fp32 statistics)."""
-    return F.layer_norm(x, (x.shape[-1],), p["gamma"].to(x.dtype), p["beta"].to(x.dtype), eps)
+    """Pre-LN LayerNorm with learned gamma / beta (bf16 in and out, fp32 statistics)."""
+    return fused.layer_norm(x, p["gamma"], p["beta"], eps)
 
 
 def attention_forward(p, x: torch.Tensor, cfg: ModelConfig) -> torch.Tensor:
@@ -146,22 +144,38 @@ def attention_forward(p, x: torch.Tensor, cfg: ModelConfig) -> torch.Tensor:
 
 
 def ffn_forward(p, x: torch.Tensor) -> torch.Tensor:
-    h = F.gelu(linear(x, p["W1"]) + p["b1"].to(x.dtype), approximate="tanh")
-    return linear(h, p["W2"]) + p["b2"].to(x.dtype)
+    """gelu_tanh(x W1 + b1) W2 + b2; bias and GELU live in the GEMM epilogues."""
+    return fused.ffn(x, p["W1"], p["b1"], p["W2"], p["b2"])
 
 
 def block_forward(p, x: torch.Tensor, cfg: ModelConfig) -> torch.Tensor:
-    x = x + attention_forward(p["attn"], layer_norm(p["ln1"], x), cfg)
-    x = x + ffn_forward(p["ffn"], layer_norm(p["ln2"], x))
-    return x
+    """One pre-LN block, x -> x + attn(LN1 x) -> (.) + ffn(LN2 .) (model.py:315-324)."""
+    x, r = _block(p, x, None, cfg)
+    return x + r
+
+
+def _block(p, x: torch.Tensor, r, cfg: ModelConfig):
+    """Block with its residual adds deferred: the stream arrives as x + r (r may
+    be None) and leaves as (x', r'); each add is folded into the next LayerNorm."""
+    if r is None:
+        h = layer_norm(p["ln1"], x, cfg.ln_eps)
+    else:
+        h, x = fused.add_layer_norm(x, r, p["ln1"]["gamma"], p["ln1"]["beta"], cfg.ln_eps)
+    a = attention_forward(p["attn"], h, cfg)
+    h2, x = fused.add_layer_norm(x, a, p["ln2"]["gamma"], p["ln2"]["beta"], cfg.ln_eps)
+    return x, ffn_forward(p["ffn"], h2)
 
 
 def model_forward_features(params, token_ids: torch.Tensor, cfg: ModelConfig = BASELINE) -> torch.Tensor:
     """Hidden states after the final LayerNorm, bf16 (bs, seq, d)."""
     x = embed(params, token_ids)
+    r = None
     for bp in params["blocks"]:
-        x = block_forward(bp, x, cfg)
-    return layer_norm(params["ln_final"], x.float()).to(COMPUTE_DTYPE)
+        x, r = _block(bp, x, r, cfg)
+    lf = params["ln_final"]
+    if r is None:
+        return layer_norm(lf, x, cfg.ln_eps)
+    return fused.add_layer_norm(x, r, lf["gamma"], lf["beta"], cfg.ln_eps)[0]
 
 
 def output_projection(params) -> torch.Tensor:

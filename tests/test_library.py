@@ -44,6 +44,26 @@ def test_status_strings_and_argument_errors_without_gpu():
     assert rc == _lib.NL_EINVAL
     with pytest.raises(_lib.NlError):
         _lib.call("nl_mean_f32", None, None, -1, None)
+    # fused epilogue: unknown mode, bias missing, GELU with beta != 0
+    args = (None, 0, 0, 4, 4, 4, 1.0, 256, 8, 512, 8, 0.0, 768, 1, 8, None)
+    assert lib.nl_gemm_fused(*args, 9, None, None, 0, None, 0) == _lib.NL_EINVAL
+    assert b"epilogue" in lib.nl_last_error()
+    assert lib.nl_gemm_fused(*args, 1, None, None, 0, None, 0) == _lib.NL_EINVAL
+    assert b"bias" in lib.nl_last_error()
+    args_beta = args[:11] + (1.0,) + args[12:]
+    assert lib.nl_gemm_fused(*args_beta, 2, 1024, 1280, 8, None, 0) == _lib.NL_EINVAL
+    assert b"beta" in lib.nl_last_error()
+    # LayerNorm width limits and workspace size
+    assert lib.nl_layernorm_fwd(None, 4, 12, 256, None, None, 512, 768, 1e-5, 1024, 1280, 1536) == _lib.NL_EINVAL
+    assert lib.nl_layernorm_fwd(None, 4, 8192, 256, None, None, 512, 768, 1e-5, 1024, 1280, 1536) == _lib.NL_EINVAL
+    assert lib.nl_layernorm_fwd(None, 4, 16, 258, None, None, 512, 768, 1e-5, 1024, 1280, 1536) == _lib.NL_EALIGN
+    assert lib.nl_layernorm_bwd_ws_bytes(16384, 512) == 2 * 1024 * 512 * 4
+    assert lib.nl_layernorm_bwd(None, 64, 512, 256, 512, 768, 1024, 1280, None, 1536, 1792, 2048, 0, 2304,
+                                16) == _lib.NL_EINVAL
+    assert b"workspace" in lib.nl_last_error()
+    assert lib.nl_colsum_ws_bytes(16384, 2048) == 256 * 2048 * 4
+    assert lib.nl_colsum_bf16(None, 8, 8, 256, 12, 512, 0, 768, 4096) == _lib.NL_EALIGN
+    assert lib.nl_embedding_fwd(None, 2, 8, 6, 100, 256, 512, 768, 1024) == _lib.NL_EINVAL
 
 
 def test_library_targets_gfx950_only():

@@ -114,3 +114,43 @@ def test_ce_vs_torch_and_invariants():
     # uniform logits give exactly ln V
     l0, _, _ = ops.ce(np.zeros((4, V)), np.arange(4))
     np.testing.assert_allclose(l0, math.log(V), rtol=1e-14)
+
+
+def test_gelu_and_layernorm_pieces_vs_torch_float64():
+    """The elementwise pieces of the model oracle against torch's own float64
+    implementations (an independent code path): tanh-GELU and its derivative,
+    LayerNorm forward and backward (dx, dgamma, dbeta)."""
+    from oracle import model_np as om
+
+    rng = np.random.default_rng(8)
+    u = rng.standard_normal(4001) * 4
+    u[:3] = [0.0, -30.0, 30.0]
+    gu, t = om._gelu(u)
+    tu = torch.from_numpy(u).requires_grad_(True)
+    ref = torch.nn.functional.gelu(tu, approximate="tanh")
+    np.testing.assert_allclose(gu, ref.detach().numpy(), rtol=1e-12, atol=1e-15)
+    ref.backward(torch.ones_like(ref))
+    np.testing.assert_allclose(om._gelu_bwd(np.ones_like(u), u, t), tu.grad.numpy(), rtol=1e-10, atol=1e-14)
+    # closed forms: gelu(0) = 0, gelu'(0) = 1/2, saturation at +-30
+    assert gu[0] == 0.0 and gu[1] == pytest.approx(0.0, abs=1e-12) and gu[2] == pytest.approx(30.0)
+
+    x = rng.standard_normal((37, 48)) * 3 + 1
+    g = rng.standard_normal(48)
+    b = rng.standard_normal(48)
+    dy = rng.standard_normal((37, 48))
+    y, cache = om._ln_fwd(x, g, b, 1e-5)
+    tx = torch.from_numpy(x).requires_grad_(True)
+    tg = torch.from_numpy(g).requires_grad_(True)
+    tb = torch.from_numpy(b).requires_grad_(True)
+    ty = torch.nn.functional.layer_norm(tx, (48,), tg, tb, 1e-5)
+    np.testing.assert_allclose(y, ty.detach().numpy(), rtol=1e-10, atol=1e-12)
+    ty.backward(torch.from_numpy(dy))
+    dx, dg, db = om._ln_bwd(dy, g, cache)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(dg, tg.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(db, tb.grad.numpy(), rtol=1e-12, atol=1e-12)
+    # invariants: dx is orthogonal to the all-ones vector; with eps = 0 also to xh
+    np.testing.assert_allclose(dx.sum(-1), 0.0, atol=1e-10)
+    _, c0 = om._ln_fwd(x, g, b, 0.0)
+    dx0, _, _ = om._ln_bwd(dy, g, c0)
+    np.testing.assert_allclose((dx0 * c0[0]).sum(-1), 0.0, atol=1e-10)
