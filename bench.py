@@ -34,12 +34,14 @@ def _args():
     ap.add_argument("--batch-size", type=int, default=32)
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
     return ap.parse_args()
 
 
 class KernelProbe:
-    """Brackets every libnlearn_hip call with HIP events on the current stream."""
+    """Brackets every libnlearn_hip call with HIP events on the current stream
+    (the stream the kernel is launched on)."""
 
     def __init__(self, torch):
         self.torch = torch
@@ -160,24 +162,36 @@ def main():
     total_updates = a.warmup + a.steps
     opt = AdamW(warmup_cosine_decay_schedule(0.0, 1e-3, 200, max(total_updates, 1000), 1e-4))
     state = opt.init(params)
-    step = make_train_step(opt, cfg)
+    graph = not a.no_graph
+    probe = KernelProbe(torch)
+    _lib.set_probe(probe)
+    step = make_train_step(opt, cfg, graph=graph, warmup=2)
     data = SyntheticTokens(bs, seq, cfg.vocab_size, seed=0, device=dev)
     batches = [data.get_batch() for _ in range(4)]
 
-    for i in range(a.warmup):
+    # warm-up (in graph mode the step is captured during it and replayed)
+    for i in range(max(a.warmup, 3 if graph else 0)):
         params, state, loss = step(params, state, batches[i % 4])
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
 
-    probe = KernelProbe(torch)
-    _lib.set_probe(probe)
-    probe.enabled = True
+    probe.enabled = not graph
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(a.steps):
         params, state, loss = step(params, state, batches[i % 4])
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    if graph:
+        # Per-kernel durations: events cannot be placed between the nodes of a
+        # replayed graph (torch-ROCm refuses external events in a capture), so
+        # the same step runs a.steps more times eagerly, every kernel bracketed
+        # by events on its launch stream; kernels and shapes are identical.
+        eager = make_train_step(opt, cfg, graph=False)
+        probe.enabled = True
+        for i in range(a.steps):
+            params, state, loss = eager(params, state, batches[i % 4])
+        torch.cuda.synchronize()
     probe.enabled = False
     _lib.set_probe(None)
 
@@ -207,7 +221,8 @@ def main():
         "dtype": "bf16",
         "data": "synthetic uniform tokens, random-init weights (seeded)",
         "config": {"workload": f"train_step fwd+bwd+AdamW d512/8h/4L vocab50257 bs{bs} seq{seq}",
-                   "global_batch": bs, "seq_len": seq, "parallelism": "single-gpu"},
+                   "global_batch": bs, "seq_len": seq, "parallelism": "single-gpu",
+                   "launch": "hip_graph" if graph else "eager"},
         "roofline": roof,
         "cpu_baseline": None,
         "detail": {

@@ -263,6 +263,29 @@ int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const floa
                   nl_bf16* p_bf16, int64_t ld_bf16, float lr, float b1, float b2, float eps, float wd,
                   float bc1, float bc2);
 
+/* The same update over a whole parameter tree in ONE launch (the optax update
+ * of train.py:504-505 applied to every leaf). The caller describes each leaf
+ * once in a table of nl_adamw_tensor; nl_adamw_multi_prepare() (host only)
+ * fills chunk0 and returns the launch size, and the table is then copied to
+ * device memory and reused every step. The per-step scalars live in device
+ * memory, hyper_dev = {lr, bc1, bc2}, so a captured HIP graph replays the
+ * update with the values the host writes there before each replay.
+ * p, g, m, v of a leaf are dense [rows][cols] fp32 and 16-byte aligned;
+ * shadow (optional) is the bf16 copy with row stride ld_shadow. */
+typedef struct nl_adamw_tensor {
+  float* p;
+  const float* g;
+  float* m;
+  float* v;
+  nl_bf16* shadow;
+  int64_t ld_shadow;
+  int64_t rows, cols;
+  int64_t chunk0;     /* first work chunk of this leaf (set by nl_adamw_multi_prepare) */
+} nl_adamw_tensor;
+int64_t nl_adamw_multi_prepare(int n_tensors, nl_adamw_tensor* tensors_host);
+int nl_adamw_multi(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
+                   const float* hyper_dev, float b1, float b2, float eps, float wd);
+
 /* ======================================================================== */
 /* LayerNorm, bias gradients, embedding                                       */
 /* ======================================================================== */

@@ -23,6 +23,14 @@ class AttnStride(ctypes.Structure):
     _fields_ = [("batch", ctypes.c_int64), ("head", ctypes.c_int64), ("row", ctypes.c_int64)]
 
 
+class AdamWTensor(ctypes.Structure):
+    """``nl_adamw_tensor``: one leaf of the multi-tensor AdamW table."""
+
+    _fields_ = [("p", ctypes.c_void_p), ("g", ctypes.c_void_p), ("m", ctypes.c_void_p), ("v", ctypes.c_void_p),
+                ("shadow", ctypes.c_void_p), ("ld_shadow", ctypes.c_int64), ("rows", ctypes.c_int64),
+                ("cols", ctypes.c_int64), ("chunk0", ctypes.c_int64)]
+
+
 class NlError(RuntimeError):
     def __init__(self, fn: str, code: int, msg: str):
         super().__init__(f"{fn} failed ({code}): {msg}")
@@ -59,6 +67,8 @@ _SIGNATURES = {
     "nl_mean_f32": [_P, _P, _I, _P],
     "nl_scale_bf16_by_device_scalar": [_P, _P, _I64, _I64, _I64, _P],
     "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F],
+    "nl_adamw_multi_prepare": [_I, _P],
+    "nl_adamw_multi": [_P, _I, _P, _I64, _P, _F, _F, _F, _F],
     "nl_layernorm_fwd": [_P, _I, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P],
     "nl_layernorm_bwd_ws_bytes": [_I, _I],
     "nl_layernorm_bwd": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t],
@@ -74,6 +84,7 @@ _RESTYPES = {
     "nl_flash_attention_bwd_ws_bytes": ctypes.c_size_t,
     "nl_gemm_ws_bytes": ctypes.c_size_t,
     "nl_layernorm_bwd_ws_bytes": ctypes.c_size_t,
+    "nl_adamw_multi_prepare": ctypes.c_int64,
     "nl_colsum_ws_bytes": ctypes.c_size_t,
 }
 

@@ -8,20 +8,27 @@
 namespace nl {
 namespace {
 
+// One element of the update. Every multiply-add is an explicit fmaf, so the
+// rounding is fixed by the source and all kernels below agree bit for bit.
+__device__ __forceinline__ void adam1(float gi, float& m, float& v, float& p, float lr, float b1, float b2, float eps,
+                                      float wd, float inv_bc1, float inv_bc2) {
+  m = __builtin_fmaf(b1, m, (1.f - b1) * gi);
+  v = __builtin_fmaf(b2, v, ((1.f - b2) * gi) * gi);
+  const float step = (m * inv_bc1) / (__builtin_sqrtf(v * inv_bc2) + eps);
+  p = __builtin_fmaf(-lr, __builtin_fmaf(wd, p, step), p);
+}
+
 __global__ __launch_bounds__(256) void adamw_kernel(int64_t rows, int64_t cols, float* __restrict__ p,
                                                     const float* __restrict__ g, float* __restrict__ m,
                                                     float* __restrict__ v, uint16_t* __restrict__ pb, int64_t ldb,
-                                                    float lr, float b1, float b2, float eps, float wd, float inv_bc1,
-                                                    float inv_bc2) {
+                                                    float lr, float b1, float b2, float eps, float wd, float bc1,
+                                                    float bc2) {
+  const float inv_bc1 = 1.f / bc1, inv_bc2 = 1.f / bc2;
   const int64_t n = rows * cols;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
-    const float gi = g[i];
-    const float mi = b1 * m[i] + (1.f - b1) * gi;
-    const float vi = b2 * v[i] + (1.f - b2) * gi * gi;
-    const float pi = p[i];
-    const float upd = (mi * inv_bc1) / (sqrtf(vi * inv_bc2) + eps) + wd * pi;
-    const float pn = pi - lr * upd;
+    float mi = m[i], vi = v[i], pn = p[i];
+    adam1(g[i], mi, vi, pn, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
     m[i] = mi;
     v[i] = vi;
     p[i] = pn;
@@ -36,17 +43,18 @@ __global__ __launch_bounds__(256) void adamw_kernel(int64_t rows, int64_t cols, 
 __global__ __launch_bounds__(256) void adamw_vec4_kernel(int64_t n4, f32x4* __restrict__ p,
                                                          const f32x4* __restrict__ g, f32x4* __restrict__ m,
                                                          f32x4* __restrict__ v, u32x2* __restrict__ pb, float lr,
-                                                         float b1, float b2, float eps, float wd, float inv_bc1,
-                                                         float inv_bc2) {
+                                                         float b1, float b2, float eps, float wd, float bc1,
+                                                         float bc2) {
+  const float inv_bc1 = 1.f / bc1, inv_bc2 = 1.f / bc2;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
-    const f32x4 gi = g[i], mo = m[i], vo = v[i], po = p[i];
-    f32x4 mi, vi, pn;
+    const f32x4 gi = g[i];
+    f32x4 mi = m[i], vi = v[i], pn = p[i];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      mi[e] = b1 * mo[e] + (1.f - b1) * gi[e];
-      vi[e] = b2 * vo[e] + (1.f - b2) * gi[e] * gi[e];
-      pn[e] = po[e] - lr * ((mi[e] * inv_bc1) / (sqrtf(vi[e] * inv_bc2) + eps) + wd * po[e]);
+      float a = mi[e], b = vi[e], c = pn[e];
+      adam1(gi[e], a, b, c, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+      mi[e] = a, vi[e] = b, pn[e] = c;
     }
     m[i] = mi;
     v[i] = vi;
@@ -55,10 +63,101 @@ __global__ __launch_bounds__(256) void adamw_vec4_kernel(int64_t n4, f32x4* __re
   }
 }
 
+constexpr int kChunk = 8192;  // elements per workgroup of the multi-tensor update
+
+// One workgroup per chunk of kChunk elements of one leaf; the leaf is found by
+// a binary search over chunk0 (the table is sorted by construction).
+__global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_tensor* __restrict__ T,
+                                                          const float* __restrict__ hyper, float b1, float b2,
+                                                          float eps, float wd) {
+  const int64_t chunk = blockIdx.x;
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (T[mid].chunk0 <= chunk) lo = mid;
+    else hi = mid - 1;
+  }
+  const nl_adamw_tensor t = T[lo];
+  const float lr = hyper[0], inv_bc1 = 1.f / hyper[1], inv_bc2 = 1.f / hyper[2];
+  const int64_t numel = t.rows * t.cols;
+  const int64_t e0 = (chunk - t.chunk0) * kChunk;
+  const int64_t e1 = min(numel, e0 + kChunk);
+  if (e0 >= e1) return;  // only with a launch larger than the prepared chunk count
+  // leaves are 16-byte aligned and chunks start at multiples of 4: vec4 body, scalar tail
+  const int64_t v1 = e0 + ((e1 - e0) & ~(int64_t)3);
+  for (int64_t e = e0 + threadIdx.x * 4; e < v1; e += 256 * 4) {
+    const f32x4 gi = *reinterpret_cast<const f32x4*>(t.g + e);
+    f32x4 m = *reinterpret_cast<const f32x4*>(t.m + e);
+    f32x4 v = *reinterpret_cast<const f32x4*>(t.v + e);
+    f32x4 p = *reinterpret_cast<const f32x4*>(t.p + e);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float mk = m[k], vk = v[k], pk = p[k];
+      adam1(gi[k], mk, vk, pk, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+      m[k] = mk, v[k] = vk, p[k] = pk;
+    }
+    *reinterpret_cast<f32x4*>(t.m + e) = m;
+    *reinterpret_cast<f32x4*>(t.v + e) = v;
+    *reinterpret_cast<f32x4*>(t.p + e) = p;
+    if (t.shadow) {
+      const int64_t r = e / t.cols, c = e - r * t.cols;
+      const int64_t o = r * t.ld_shadow + c;
+      if (c + 4 <= t.cols && (o & 3) == 0) {
+        *reinterpret_cast<u32x2*>(t.shadow + o) = u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int64_t rk = (e + k) / t.cols, ck = e + k - rk * t.cols;
+          t.shadow[rk * t.ld_shadow + ck] = f32_to_bf16(p[k]);
+        }
+      }
+    }
+  }
+  for (int64_t e = v1 + threadIdx.x; e < e1; e += 256) {
+    float m = t.m[e], v = t.v[e], p = t.p[e];
+    adam1(t.g[e], m, v, p, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+    t.m[e] = m;
+    t.v[e] = v;
+    t.p[e] = p;
+    if (t.shadow) {
+      const int64_t r = e / t.cols, c = e - r * t.cols;
+      t.shadow[r * t.ld_shadow + c] = f32_to_bf16(p);
+    }
+  }
+}
+
 }  // namespace
 }  // namespace nl
 
 using namespace nl;
+
+extern "C" int64_t nl_adamw_multi_prepare(int n_tensors, nl_adamw_tensor* T) {
+  if (n_tensors < 0 || (n_tensors > 0 && !T)) return -(int64_t)nl_set_error(NL_EINVAL, "adamw_multi: bad table");
+  int64_t chunks = 0;
+  for (int i = 0; i < n_tensors; ++i) {
+    if (T[i].rows < 0 || T[i].cols < 0) return -(int64_t)nl_set_error(NL_EINVAL, "adamw_multi: negative size");
+    if (!T[i].p || !T[i].g || !T[i].m || !T[i].v)
+      return -(int64_t)nl_set_error(NL_EINVAL, "adamw_multi: null pointer in the table");
+    if ((((uintptr_t)T[i].p | (uintptr_t)T[i].g | (uintptr_t)T[i].m | (uintptr_t)T[i].v) & 15) != 0)
+      return -(int64_t)nl_set_error(NL_EALIGN, "adamw_multi: p, g, m, v must be 16-byte aligned");
+    if (T[i].shadow && (T[i].ld_shadow < T[i].cols || ((uintptr_t)T[i].shadow & 7) != 0))
+      return -(int64_t)nl_set_error(NL_EINVAL, "adamw_multi: shadow needs ld_shadow >= cols and 8-byte alignment");
+    T[i].chunk0 = chunks;
+    chunks += (T[i].rows * T[i].cols + kChunk - 1) / kChunk;
+  }
+  return chunks;
+}
+
+extern "C" int nl_adamw_multi(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
+                              const float* hyper_dev, float b1, float b2, float eps, float wd) {
+  if (n_tensors < 0 || n_chunks < 0) return nl_set_error(NL_EINVAL, "adamw_multi: negative count");
+  if (n_tensors == 0 || n_chunks == 0) return NL_OK;
+  if (!tensors_dev || !hyper_dev) return nl_set_error(NL_EINVAL, "adamw_multi: null pointer");
+  if (n_chunks > 0x7fffffff) return nl_set_error(NL_EINVAL, "adamw_multi: too many chunks");
+  hipLaunchKernelGGL(adamw_multi_kernel, dim3((unsigned)n_chunks), dim3(256), 0, (hipStream_t)stream, n_tensors,
+                     tensors_dev, hyper_dev, b1, b2, eps, wd);
+  return nl_check_launch("nl_adamw_multi");
+}
 
 extern "C" int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const float* g, float* m, float* v,
                              nl_bf16* p_bf16, int64_t ld_bf16, float lr, float b1, float b2, float eps, float wd,
@@ -77,12 +176,11 @@ extern "C" int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p,
     const int64_t n4 = n / 4;
     const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 8192);
     hipLaunchKernelGGL(adamw_vec4_kernel, dim3((unsigned)blocks), dim3(256), 0, st, n4, (f32x4*)p,
-                       (const f32x4*)g, (f32x4*)m, (f32x4*)v, (u32x2*)p_bf16, lr, b1, b2, eps, wd, 1.f / bc1,
-                       1.f / bc2);
+                       (const f32x4*)g, (f32x4*)m, (f32x4*)v, (u32x2*)p_bf16, lr, b1, b2, eps, wd, bc1, bc2);
   } else {
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
     hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)blocks), dim3(256), 0, st, rows, cols, p, g, m, v, p_bf16,
-                       p_bf16 ? ld_bf16 : cols, lr, b1, b2, eps, wd, 1.f / bc1, 1.f / bc2);
+                       p_bf16 ? ld_bf16 : cols, lr, b1, b2, eps, wd, bc1, bc2);
   }
   return nl_check_launch("nl_adamw_step");
 }

@@ -19,7 +19,7 @@ import torch
 
 from .. import _lib
 from .gemm import (EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU, _check_device, _kernel_ready, _ld, bf16_shadow, gemm_raw,
-                   padded_empty)
+                   grad_buffer, padded_empty)
 
 _BF16 = torch.bfloat16
 _F32 = torch.float32
@@ -65,12 +65,14 @@ def layer_norm_fwd_raw(x2, gamma, beta, eps, residual=None):
     return y, s, mean, rstd
 
 
-def layer_norm_bwd_raw(dy2, xin, mean, rstd, gamma, dres=None):
-    """-> dx (+ dres), dgamma, dbeta."""
+def layer_norm_bwd_raw(dy2, xin, mean, rstd, gamma, dres=None, dgamma=None, dbeta=None):
+    """-> dx (+ dres), dgamma, dbeta (written into the given buffers if any)."""
     rows, D = dy2.shape
     dx = torch.empty_like(dy2)
-    dgamma = torch.empty(D, dtype=_F32, device=dy2.device)
-    dbeta = torch.empty(D, dtype=_F32, device=dy2.device)
+    if dgamma is None:
+        dgamma = torch.empty(D, dtype=_F32, device=dy2.device)
+    if dbeta is None:
+        dbeta = torch.empty(D, dtype=_F32, device=dy2.device)
     wsb = int(_lib.load().nl_layernorm_bwd_ws_bytes(rows, D))
     ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=dy2.device)
     _lib.call("nl_layernorm_bwd", _stream(dy2), rows, D, dy2.data_ptr(), xin.data_ptr(), mean.data_ptr(),
@@ -87,13 +89,14 @@ class _LayerNorm(torch.autograd.Function):
         y, _, mean, rstd = layer_norm_fwd_raw(x2, g, b, eps)
         ctx.save_for_backward(x2, mean, rstd, g)
         ctx.shape = x.shape
+        ctx.bufs = (grad_buffer(gamma), grad_buffer(beta))
         return y.view(x.shape)
 
     @staticmethod
     def backward(ctx, dy):
         x2, mean, rstd, g = ctx.saved_tensors
-        dx, dg, db = layer_norm_bwd_raw(_rows(dy), x2, mean, rstd, g)
-        return dx.view(ctx.shape), dg, db, None
+        dx, dg, db = layer_norm_bwd_raw(_rows(dy), x2, mean, rstd, g, None, *ctx.bufs)
+        return dx.view(ctx.shape), *_unless_buffered(ctx.bufs, (dg, db)), None
 
 
 class _AddLayerNorm(torch.autograd.Function):
@@ -107,6 +110,7 @@ class _AddLayerNorm(torch.autograd.Function):
         y, s, mean, rstd = layer_norm_fwd_raw(x2, g, b, eps, residual=r2)
         ctx.save_for_backward(s, mean, rstd, g)
         ctx.shape = x.shape
+        ctx.bufs = (grad_buffer(gamma), grad_buffer(beta))
         return y.view(x.shape), s.view(x.shape)
 
     @staticmethod
@@ -115,9 +119,15 @@ class _AddLayerNorm(torch.autograd.Function):
         if dy is None:
             dx = _rows(ds)
             return dx.view(ctx.shape), dx.view(ctx.shape), None, None, None
-        dx, dg, db = layer_norm_bwd_raw(_rows(dy), s, mean, rstd, g, dres=_rows(ds) if ds is not None else None)
+        dx, dg, db = layer_norm_bwd_raw(_rows(dy), s, mean, rstd, g, _rows(ds) if ds is not None else None,
+                                        *ctx.bufs)
         dx = dx.view(ctx.shape)
-        return dx, dx, dg, db, None
+        return dx, dx, *_unless_buffered(ctx.bufs, (dg, db)), None
+
+
+def _unless_buffered(bufs, grads):
+    """Gradients to hand back to autograd: None where a main_grad buffer took them."""
+    return tuple(None if b is not None else g for b, g in zip(bufs, grads))
 
 
 def layer_norm(x: torch.Tensor, gamma: torch.Tensor, beta: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
@@ -136,11 +146,12 @@ def add_layer_norm(x: torch.Tensor, r: torch.Tensor, gamma: torch.Tensor, beta: 
 # ---------------------------------------------------------------------------
 
 
-def colsum(x2: torch.Tensor) -> torch.Tensor:
+def colsum(x2: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 column sums of a bf16 [rows, cols] matrix (fixed summation order)."""
     rows, cols = x2.shape
     x2 = _kernel_ready(x2)
-    out = torch.empty(cols, dtype=_F32, device=x2.device)
+    if out is None:
+        out = torch.empty(cols, dtype=_F32, device=x2.device)
     wsb = int(_lib.load().nl_colsum_ws_bytes(rows, cols))
     ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=x2.device)
     _lib.call("nl_colsum_bf16", _stream(x2), rows, cols, x2.data_ptr(), _ld(x2), out.data_ptr(), 0, ws.data_ptr(),
@@ -165,24 +176,26 @@ class _FFN(torch.autograd.Function):
         gemm_raw(x2, W1b, out=h, epi=EPI_BIAS_GELU, bias=b1f, aux=u)
         y = padded_empty(M, W2b.shape[1], _BF16, x2.device)
         gemm_raw(h, W2b, out=y, epi=EPI_BIAS, bias=b2f)
-        ctx.save_for_backward(x2, u, h, W1, W2)
+        ctx.save_for_backward(x2, u, h)
         ctx.wb = (W1b, W2b)
+        ctx.bufs = tuple(grad_buffer(t) for t in (W1, b1, W2, b2))
         ctx.shape = x.shape
         return y.view(*x.shape[:-1], W2b.shape[1])
 
     @staticmethod
     def backward(ctx, dy):
-        x2, u, h, W1, W2 = ctx.saved_tensors
+        x2, u, h = ctx.saved_tensors
         W1b, W2b = ctx.wb
+        gW1, gb1, gW2, gb2 = ctx.bufs
         dy2 = _rows(dy)
-        db2 = colsum(dy2)
-        dW2 = gemm_raw(h, dy2, "T", "N", out_dtype=_F32)                          # h^T . dy
+        db2 = colsum(dy2, out=gb2)
+        dW2 = gemm_raw(h, dy2, "T", "N", out_dtype=_F32, out=gW2)                 # h^T . dy
         du = padded_empty(u.shape[0], u.shape[1], _BF16, dy2.device)
         gemm_raw(dy2, W2b, "N", "T", out=du, epi=EPI_DGELU, aux=u)               # (dy . W2^T) * gelu'(u)
-        db1 = colsum(du)
-        dW1 = gemm_raw(x2, du, "T", "N", out_dtype=_F32)                          # x^T . du
+        db1 = colsum(du, out=gb1)
+        dW1 = gemm_raw(x2, du, "T", "N", out_dtype=_F32, out=gW1)                 # x^T . du
         dx = gemm_raw(du, W1b, "N", "T", out_dtype=_BF16)                          # du . W1^T
-        return dx.view(ctx.shape), dW1, db1, dW2, db2
+        return dx.view(ctx.shape), *_unless_buffered(ctx.bufs, (dW1, db1, dW2, db2))
 
 
 def ffn(x: torch.Tensor, W1: torch.Tensor, b1: torch.Tensor, W2: torch.Tensor, b2: torch.Tensor) -> torch.Tensor:
@@ -210,6 +223,7 @@ class _Embedding(torch.autograd.Function):
                   out.data_ptr())
         ctx.save_for_backward(ids32)
         ctx.dims = (B, S, D, V, tuple(pos.shape))
+        ctx.bufs = (grad_buffer(tok), grad_buffer(pos))
         return out
 
     @staticmethod
@@ -217,11 +231,13 @@ class _Embedding(torch.autograd.Function):
         (ids32,) = ctx.saved_tensors
         B, S, D, V, pshape = ctx.dims
         dx = dx.to(_BF16).contiguous()
-        dtok = torch.zeros((V, D), dtype=_F32, device=dx.device)
-        dpos = torch.zeros(pshape, dtype=_F32, device=dx.device)
+        gt, gp = ctx.bufs
+        # zero_() is a fill kernel (no memset node when the step is captured)
+        dtok = gt.zero_() if gt is not None else torch.zeros((V, D), dtype=_F32, device=dx.device)
+        dpos = gp.zero_() if gp is not None else torch.zeros(pshape, dtype=_F32, device=dx.device)
         _lib.call("nl_embedding_bwd", _stream(dx), B, S, D, V, ids32.data_ptr(), dx.data_ptr(), dtok.data_ptr(),
                   dpos.data_ptr(), 0)
-        return None, dtok, dpos
+        return None, *_unless_buffered(ctx.bufs, (dtok, dpos))
 
 
 def embedding(ids: torch.Tensor, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:

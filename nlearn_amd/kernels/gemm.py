@@ -144,6 +144,15 @@ def bf16_shadow(W: torch.Tensor) -> torch.Tensor:
     return sh
 
 
+def grad_buffer(W: torch.Tensor) -> torch.Tensor | None:
+    """W's preallocated fp32 gradient buffer (``W.main_grad``), or None.
+
+    The optimizer attaches these once (fixed addresses, so a captured step
+    writes the same memory every replay); a backward that finds one writes the
+    weight gradient straight into it and returns no gradient to autograd."""
+    return getattr(W, "main_grad", None)
+
+
 # ---------------------------------------------------------------------------
 # gemm — gemm.py:61-79
 # ---------------------------------------------------------------------------
@@ -205,7 +214,11 @@ class _Linear(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             dx = gemm_raw(dy, Wb, "N", "T", out_dtype=x2.dtype)             # dY . W^T
         if ctx.needs_input_grad[1]:
-            dW = gemm_raw(x2, dy, "T", "N", out_dtype=_F32 if W.dtype == _F32 else W.dtype)  # X^T . dY
+            mg = grad_buffer(W)
+            if mg is not None:
+                gemm_raw(x2, dy, "T", "N", out=mg)                                 # X^T . dY -> main_grad
+            else:
+                dW = gemm_raw(x2, dy, "T", "N", out_dtype=_F32 if W.dtype == _F32 else W.dtype)
         return dx, dW
 
 

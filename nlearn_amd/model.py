@@ -110,10 +110,24 @@ def init_params_numpy(seed: int = 0, cfg: ModelConfig = BASELINE) -> dict:
     return tree_map(lambda _: next(it), shapes)
 
 
+def device_param(a: np.ndarray, device="cuda") -> torch.Tensor:
+    """A leaf parameter on the device. A matrix whose row is not a whole number
+    of 16-byte chunks (the LM head: 50257 columns) is stored with its row
+    stride rounded up to 8 elements, so the GEMMs, the gradient buffer and the
+    optimizer all address it with aligned rows; the padding stays zero."""
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if t.dim() == 2 and t.shape[1] % 8:
+        rows, cols = t.shape
+        base = torch.zeros((rows, (cols + 7) // 8 * 8), dtype=t.dtype, device=device)
+        base[:, :cols] = t.to(device)
+        return base[:, :cols].requires_grad_(True)
+    return t.to(device).requires_grad_(True)
+
+
 def init_model(seed: int = 0, cfg: ModelConfig = BASELINE, device="cuda") -> dict:
     """fp32 device parameters, requires_grad, seeded through NumPy so a CPU
     restatement can start from the identical weights."""
-    return tree_map(lambda a: torch.from_numpy(a).to(device).requires_grad_(True), init_params_numpy(seed, cfg))
+    return tree_map(lambda a: device_param(a, device), init_params_numpy(seed, cfg))
 
 
 def count_params(params) -> int:

@@ -68,58 +68,164 @@ def warmup_cosine_decay_schedule(init_value: float, peak_value: float, warmup_st
     return schedule
 
 
+def _rows_ld(t: torch.Tensor):
+    """(rows, row stride) of a leaf as the kernels address it: a 2-D tensor with
+    unit column stride is rows x stride(0) dense over its storage (padding
+    included); anything else is one dense row."""
+    if t.dim() == 2 and t.stride(1) == 1 and t.shape[0] > 1:
+        return t.shape[0], t.stride(0)
+    return 1, t.numel()
+
+
+def _zeros_with_layout(p: torch.Tensor) -> torch.Tensor:
+    """fp32 zeros with p's row layout (a padded matrix stays padded)."""
+    rows, ld = _rows_ld(p)
+    base = torch.zeros(rows * ld, dtype=torch.float32, device=p.device)
+    if p.dim() == 2 and ld != p.shape[1]:
+        return base.view(rows, ld)[:, :p.shape[1]]
+    return base.view(p.shape)
+
+
+def attach_grad_buffers(params) -> torch.Tensor:
+    """Give every leaf a ``main_grad``: a view into ONE zeroed fp32 buffer, laid
+    out like the leaf (64-element aligned starts). The model's backward writes
+    each weight gradient straight into it, at the same address every step."""
+    leaves = tree_leaves(params)
+    sizes = []
+    for p in leaves:
+        rows, ld = _rows_ld(p)
+        sizes.append((rows * ld + 63) // 64 * 64)
+    flat = torch.zeros(sum(sizes), dtype=torch.float32, device=leaves[0].device)
+    off = 0
+    for p, n in zip(leaves, sizes):
+        rows, ld = _rows_ld(p)
+        seg = flat[off:off + rows * ld]
+        if p.dim() == 2 and ld != p.shape[1]:
+            p.main_grad = seg.view(rows, ld)[:, :p.shape[1]]
+        else:
+            p.main_grad = seg.view(p.shape)
+        off += n
+    return flat
+
+
 class AdamW:
     """optax.adamw(learning_rate=schedule, b1=.9, b2=.999, eps=1e-8, weight_decay)
     with decoupled decay on every parameter. The schedule is evaluated at the
     update count before the update (optax's ``count``), bias corrections use the
-    count after it."""
+    count after it.
+
+    ``init`` attaches fixed gradient buffers to the leaves (``main_grad``); the
+    update is then ONE multi-tensor launch that reads lr and the bias
+    corrections from device memory (``state["hyper"]``), so it can live inside
+    a captured HIP graph. ``prepare`` writes those scalars for the coming
+    update, ``apply`` launches it, ``update`` does both and counts the step.
+    Leaves without a buffer fall back to one launch per leaf on ``.grad``."""
 
     def __init__(self, learning_rate, weight_decay: float = WEIGHT_DECAY, b1: float = 0.9, b2: float = 0.999,
-                 eps: float = 1e-8):
+                 eps: float = 1e-8, grad_buffers: bool = True):
         self.lr = learning_rate if callable(learning_rate) else (lambda _c, v=learning_rate: v)
         self.wd, self.b1, self.b2, self.eps = weight_decay, b1, b2, eps
+        self.grad_buffers = grad_buffers
 
     def init(self, params) -> dict:
         leaves = tree_leaves(params)
+        flat = attach_grad_buffers(params) if self.grad_buffers else None
         return {"count": 0,
-                "mu": [torch.zeros_like(p, dtype=torch.float32) for p in leaves],
-                "nu": [torch.zeros_like(p, dtype=torch.float32) for p in leaves]}
+                "mu": [_zeros_with_layout(p) for p in leaves],
+                "nu": [_zeros_with_layout(p) for p in leaves],
+                "grad_flat": flat,
+                "hyper": torch.ones(3, dtype=torch.float32, device=leaves[0].device),
+                "table": None}
 
-    def update(self, params, state: dict) -> dict:
-        """Apply one step in place using each parameter's ``.grad``."""
-        count = state["count"]
-        lr = float(self.lr(count))
+    def hyper_values(self, count: int):
         t = count + 1
-        bc1, bc2 = 1.0 - self.b1 ** t, 1.0 - self.b2 ** t
-        for p, m, v in zip(tree_leaves(params), state["mu"], state["nu"]):
-            g = p.grad
+        return float(self.lr(count)), 1.0 - self.b1 ** t, 1.0 - self.b2 ** t
+
+    def prepare(self, state: dict) -> None:
+        """Write {lr, bc1, bc2} of update ``state["count"] + 1`` to the device
+        (an async copy from freshly pinned memory, ordered on the stream)."""
+        h = torch.tensor(self.hyper_values(state["count"]), dtype=torch.float32).pin_memory()
+        state["hyper"].copy_(h, non_blocking=True)
+
+    def _table(self, params, state):
+        """Device table of the multi-tensor update, rebuilt when a bf16 shadow changed."""
+        leaves = tree_leaves(params)
+        shadows = []
+        for p in leaves:
+            sh = getattr(p, "_nl_bf16", None)
+            shadows.append(sh if sh is not None and getattr(p, "_nl_bf16_version", None) == p._version else None)
+        key = tuple(sh.data_ptr() if sh is not None else 0 for sh in shadows)
+        cached = state["table"]
+        if cached is not None and cached[0] == key:
+            return cached
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("AdamW: parameter layout changed during graph capture")
+        T = (_lib.AdamWTensor * len(leaves))()
+        for i, (p, m, v, sh) in enumerate(zip(leaves, state["mu"], state["nu"], shadows)):
+            rows, ld = _rows_ld(p)
+            g = p.main_grad
+            if _rows_ld(g) != (rows, ld) or _rows_ld(m) != (rows, ld):
+                raise RuntimeError("AdamW: gradient / moment layout differs from the parameter's")
+            T[i].p, T[i].g, T[i].m, T[i].v = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()
+            T[i].rows, T[i].cols = rows, ld
+            if sh is not None:
+                T[i].shadow, T[i].ld_shadow = sh.data_ptr(), _rows_ld(sh)[1]
+        n_chunks = int(_lib.load().nl_adamw_multi_prepare(len(leaves), T))
+        if n_chunks < 0:
+            raise _lib.NlError("nl_adamw_multi_prepare", -n_chunks, _lib.load().nl_last_error().decode())
+        dev_table = torch.frombuffer(bytearray(T), dtype=torch.uint8).to(leaves[0].device)
+        state["table"] = (key, dev_table, len(leaves), n_chunks)
+        return state["table"]
+
+    def apply(self, params, state: dict) -> None:
+        """Launch the update with the scalars already on the device (no host sync)."""
+        leaves = tree_leaves(params)
+        stream = torch.cuda.current_stream(leaves[0].device).cuda_stream
+        if all(getattr(p, "main_grad", None) is not None for p in leaves):
+            _, table, n, n_chunks = self._table(params, state)
+            _lib.call("nl_adamw_multi", stream, n, table.data_ptr(), n_chunks, state["hyper"].data_ptr(),
+                      self.b1, self.b2, self.eps, self.wd)
+            return
+        lr, bc1, bc2 = self.hyper_values(state["count"])
+        for p, m, v in zip(leaves, state["mu"], state["nu"]):
+            g = getattr(p, "main_grad", None)
+            g = p.grad if g is None else g
             if g is None:
                 continue
-            if not g.is_contiguous():
-                g = g.contiguous()
+            if g.stride() != p.stride():
+                g2 = _zeros_with_layout(p)
+                g2.copy_(g)
+                g = g2
+            rows, ld = _rows_ld(p)
             shadow = getattr(p, "_nl_bf16", None)
-            rows = p.shape[0] if p.dim() == 2 else 1
-            cols = p.shape[1] if p.dim() == 2 else p.numel()
             sb, ldb = (None, 0)
             if shadow is not None and getattr(p, "_nl_bf16_version", None) == p._version:
-                sb, ldb = shadow.data_ptr(), (shadow.stride(0) if shadow.dim() == 2 else cols)
-            _lib.call("nl_adamw_step", torch.cuda.current_stream(p.device).cuda_stream, rows, cols,
-                      p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), sb, ldb, lr, self.b1, self.b2,
-                      self.eps, self.wd, bc1, bc2)
-        state["count"] = t
+                sb, ldb = shadow.data_ptr(), _rows_ld(shadow)[1]
+            _lib.call("nl_adamw_step", stream, rows, ld, p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
+                      sb, ldb, lr, self.b1, self.b2, self.eps, self.wd, bc1, bc2)
+
+    def update(self, params, state: dict) -> dict:
+        """Apply one step in place (gradients from ``main_grad`` or ``.grad``)."""
+        self.prepare(state)
+        self.apply(params, state)
+        state["count"] += 1
         return state
 
 
-def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE):
+def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool = False, warmup: int = 2):
     """train_step(params, opt_state, batch) -> (params, opt_state, loss).
 
     Parameters are updated in place; the loss is a 0-d device tensor (no host
     sync inside the step, as with the jitted step of train.py:328-341).
+
+    graph=True: after ``warmup`` eager steps the whole step (forward, backward,
+    AdamW) is captured once into a HIP graph and replayed; the batch is copied
+    into the graph's input buffer and lr / bias corrections are written to the
+    device before each replay.
     """
 
-    def train_step(params, opt_state, batch):
-        leaves = tree_leaves(params)
-        for p in leaves:
+    def eager_step(params, opt_state, batch):
+        for p in tree_leaves(params):
             p.grad = None
         loss = batch_loss(params, batch, cfg)
         loss.backward()
@@ -127,7 +233,47 @@ def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE):
             opt_state = optimizer.update(params, opt_state)
         return params, opt_state, loss.detach()
 
-    return train_step
+    if not graph:
+        return eager_step
+    return _GraphedStep(optimizer, cfg, eager_step, warmup)
+
+
+class _GraphedStep:
+    def __init__(self, optimizer, cfg, eager_step, warmup):
+        self.opt, self.cfg, self.eager_step, self.warmup = optimizer, cfg, eager_step, warmup
+        self.done = 0
+        self.graph = None
+        self.static_batch = None
+        self.static_loss = None
+
+    def _capture(self, params, state, batch):
+        leaves = tree_leaves(params)
+        if not all(getattr(p, "main_grad", None) is not None for p in leaves):
+            raise RuntimeError("graph capture needs the optimizer's gradient buffers (AdamW(grad_buffers=True))")
+        self.static_batch = batch.detach().clone()
+        for p in leaves:
+            p.grad = None
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            loss = batch_loss(params, self.static_batch, self.cfg)
+            loss.backward()
+            with torch.no_grad():
+                self.opt.apply(params, state)
+        self.static_loss = loss.detach()
+        self.graph = g
+
+    def __call__(self, params, state, batch):
+        if self.graph is None:
+            if self.done < self.warmup:
+                self.done += 1
+                return self.eager_step(params, state, batch)
+            self._capture(params, state, batch)
+        self.static_batch.copy_(batch, non_blocking=True)
+        self.opt.prepare(state)
+        self.graph.replay()
+        state["count"] += 1
+        return params, state, self.static_loss.clone()
 
 
 # ---------------------------------------------------------------------------

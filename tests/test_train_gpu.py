@@ -43,7 +43,8 @@ def test_first_step_gradients_match_oracle(dev):
         assert err < 5e-2, (name, err)
 
 
-def test_loss_curve_matches_oracle_over_20_steps(dev):
+@pytest.mark.parametrize("graph", [False, True], ids=["eager", "hip_graph"])
+def test_loss_curve_matches_oracle_over_20_steps(dev, graph):
     import torch
     from nlearn_amd.model import init_model
     from nlearn_amd.train import AdamW, make_train_step, warmup_cosine_decay_schedule
@@ -53,7 +54,7 @@ def test_loss_curve_matches_oracle_over_20_steps(dev):
     opt = AdamW(sched)
     params = init_model(0, device=dev)
     state = opt.init(params)
-    step = make_train_step(opt)
+    step = make_train_step(opt, graph=graph)
     gpu = []
     for b in batches:
         params, state, loss = step(params, state, torch.from_numpy(b).to(dev))
