@@ -585,7 +585,15 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int FM = WTM / 32, FN = WTN / 32;
   constexpr int STAGE = (BM + BN) * BKT;  // elements per stage
-  __shared__ __attribute__((aligned(16))) uint16_t smem[S * STAGE];
+  // After the K loop the same LDS holds the epilogue: four 8 KB store slabs at
+  // byte 0 and, from byte kExtra, the bias columns (1 KB) or the saved GELU
+  // pre-activation tile (32 KB).
+  constexpr bool kBias = EPI == NL_EPI_BIAS || EPI == NL_EPI_BIAS_GELU;
+  constexpr bool kAux = EPI == NL_EPI_DGELU;
+  constexpr int kExtra = 32768;
+  constexpr int kEpiBytes = kExtra + (kAux ? BM * BN * 2 : kBias ? 1024 : 0);
+  constexpr int kSmem = S * STAGE * 2 > kEpiBytes ? S * STAGE : kEpiBytes / 2;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -719,18 +727,16 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   // into LDS by DMA before the first store: a wait on a vector load also waits
   // for every earlier store, so loads mixed into the store stream would
   // serialise it. The operand tiles' LDS is free once all waves pass the barrier.
-  constexpr bool kBias = EPI == NL_EPI_BIAS || EPI == NL_EPI_BIAS_GELU;
-  constexpr bool kAux = EPI == NL_EPI_DGELU;
-  static_assert(!kAux || S * STAGE * 2 >= BM * BN * 2, "aux tile must fit the pipeline LDS");
-  static_assert(BN == 128, "the staged epilogue assumes 128-column tiles");
-  const float* sbias = reinterpret_cast<const float*>(smem);
+  static_assert((!kBias && !kAux) || (BM == 128 && BN == 128), "the staged epilogue assumes 128 x 128 tiles");
+  uint16_t* const xlds = smem + kExtra / 2;
+  const float* sbias = reinterpret_cast<const float*>(xlds);
+  __syncthreads();
   if constexpr (kBias || kAux) {
-    __syncthreads();
     if constexpr (kBias) {
       // bias[n0 .. n0+255] -> 1 KB (only the first 128 are read); clipped at N
       if (wave == 0) {
         const __amdgpu_buffer_rsrc_t rbias = make_rsrc(g.bias, (uint32_t)g.N * 4u);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rbias, (lds_void*)smem, 16, (uint32_t)(n0 + lane * 4) * 4u, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rbias, (lds_void*)xlds, 16, (uint32_t)(n0 + lane * 4) * 4u, 0, 0, 0);
       }
     } else {
       // aux tile [128][128] bf16: row r at r*256 bytes, 16-byte chunk c at slot c ^ (r & 15)
@@ -742,7 +748,7 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
         const int r = blk * 4 + (lane >> 4);
         const int c = (lane & 15) ^ (r & 15);
         const uint32_t off = (uint32_t)(((int64_t)(m0 + r) * g.ldaux + n0 + c * 8) * 2);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(raux, (lds_void*)(smem + blk * 512), 16, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(raux, (lds_void*)(xlds + blk * 512), 16, off, 0, 0, 0);
       }
     }
     wait_vm<0>();
@@ -750,28 +756,137 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   }
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
+  if (g.beta != 0.f) {
+    // C is read back: per-lane path (the reads sit between the stores)
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int ml = wm * WTM + i * 32 + frow;
-    const int m = m0 + ml;
-    if (m >= g.M) continue;
+    for (int i = 0; i < FM; ++i) {
+      const int ml = wm * WTM + i * 32 + frow;
+      const int m = m0 + ml;
+      if (m >= g.M) continue;
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
+      for (int j = 0; j < FN; ++j) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int nl = wn * WTN + j * 32 + q * 8 + g4;
-        const int n = n0 + nl;
-        if (n >= g.N) continue;
-        float v[4] = {acc[i][j][4 * q + 0] * s, acc[i][j][4 * q + 1] * s, acc[i][j][4 * q + 2] * s,
-                      acc[i][j][4 * q + 3] * s};
-        f32x4 b = {0.f, 0.f, 0.f, 0.f};
-        u32x2 a = {0u, 0u};
-        if constexpr (kBias) b = *reinterpret_cast<const f32x4*>(sbias + nl);
-        if constexpr (kAux)
-          a = *reinterpret_cast<const u32x2*>(smem + ml * 128 + (((nl >> 3) ^ (ml & 15)) << 3) + (nl & 7));
-        epilogue_apply<OutT, EPI>(g, m, n, v, b, a);
+        for (int q = 0; q < 4; ++q) {
+          const int nl = wn * WTN + j * 32 + q * 8 + g4;
+          const int n = n0 + nl;
+          if (n >= g.N) continue;
+          float v[4] = {acc[i][j][4 * q + 0] * s, acc[i][j][4 * q + 1] * s, acc[i][j][4 * q + 2] * s,
+                        acc[i][j][4 * q + 3] * s};
+          f32x4 b = {0.f, 0.f, 0.f, 0.f};
+          if constexpr (kBias) b = *reinterpret_cast<const f32x4*>(sbias + nl);
+          epilogue_apply<OutT, EPI>(g, m, n, v, b, u32x2{0u, 0u});
+        }
       }
     }
+    return;
+  }
+
+  // Row-coalesced stores through LDS. A lane's MFMA results are 4-column
+  // pieces of 32 different rows; storing them directly makes every store
+  // instruction touch 32 rows. Instead each wave writes its 32-row slab (one
+  // MFMA row block) into a private 8 KB LDS region, 16-byte chunks XOR-swizzled
+  // by row, and reads it back so that consecutive lanes hold consecutive
+  // 16-byte pieces of a row. Values are finished (scale, bias, GELU') group by
+  // group on the way into LDS, which keeps few of them live in VGPRs.
+  static_assert(WTN == 64, "the store transpose assumes 64-column wave tiles");
+  uint8_t* wl = reinterpret_cast<uint8_t*>(smem) + wave * 8192;
+  auto finish4 = [&](int i, int j, int q, float x[4]) {
+    const int nl = wn * WTN + j * 32 + q * 8 + g4;
+    f32x4 b = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (kBias) b = *reinterpret_cast<const f32x4*>(sbias + nl);
+    u32x2 a = {0u, 0u};
+    if constexpr (kAux) {
+      const int ml = wm * WTM + i * 32 + frow;
+      a = *reinterpret_cast<const u32x2*>(xlds + ml * 128 + (((nl >> 3) ^ (ml & 15)) << 3) + (nl & 7));
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[e] = acc[i][j][4 * q + e] * s;
+      if constexpr (kBias) x[e] += b[e];
+      if constexpr (kAux) x[e] *= gelu_tanh_grad(e & 1 ? bf16_hi(a[e >> 1]) : bf16_lo(a[e >> 1]));
+    }
+  };
+  // write the lane's 4 values of (slab row frow, columns j*32 + q*8 + g4 ..) into the slab
+  auto at_bf16 = [&](int j, int q) {
+    const int c = j * 32 + q * 8 + g4;                  // 128-byte rows, 8 chunks
+    return reinterpret_cast<u32x2*>(wl + frow * 128 + ((((c * 2) >> 4) ^ (frow & 7)) << 4) + ((c * 2) & 15));
+  };
+  auto put_bf16 = [&](int j, int q, const float x[4]) {
+    *at_bf16(j, q) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+  };
+  auto put_f32 = [&](int j, int q, const float x[4]) {
+    const int c = j * 32 + q * 8 + g4;                  // 256-byte rows, 16 chunks
+    *reinterpret_cast<f32x4*>(wl + frow * 256 + ((((c * 4) >> 4) ^ (frow & 15)) << 4)) = f32x4{x[0], x[1], x[2], x[3]};
+  };
+  // copy slab i (32 rows) from LDS to global rows, 16 bytes per lane
+  auto copy_out = [&](auto tag, int i, void* base, int64_t ld) {
+    using T = decltype(tag);
+    constexpr int PITCH = WTN * (int)sizeof(T);
+    constexpr int CPR = PITCH / 16;
+    constexpr int EPC = 16 / (int)sizeof(T);
+    constexpr int RPI = 64 / CPR;                       // slab rows per instruction
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int r = it * RPI + lane / CPR;
+      const int ch = lane % CPR;
+      const u32x4 val = *reinterpret_cast<const u32x4*>(wl + r * PITCH + ((ch ^ (r & (CPR - 1))) << 4));
+      const int m = m0 + wm * WTM + i * 32 + r;
+      const int n = n0 + wn * WTN + ch * EPC;
+      if (m >= g.M || n >= g.N) continue;
+      T* dst = reinterpret_cast<T*>(base) + (int64_t)m * ld + n;
+      if (n + EPC <= g.N) {
+        __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+      } else {
+#pragma unroll
+        for (int k = 0; k < EPC; ++k) {
+          if (n + k >= g.N) break;
+          if constexpr (sizeof(T) == 2) dst[k] = (T)(val[k >> 1] >> (16 * (k & 1)));
+          else dst[k] = __uint_as_float(val[k]);
+        }
+      }
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    if constexpr (EPI == NL_EPI_BIAS_GELU) {
+      // the pre-activation u = bf16(v + bias) goes to aux; C = gelu(u), with u
+      // read back from the lane's own slab entries
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float x[4];
+          finish4(i, j, q, x);
+          put_bf16(j, q, x);
+        }
+      copy_out(uint16_t{}, i, g.aux, g.ldaux);
+      u32x2 uu[FN][4];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) uu[j][q] = *at_bf16(j, q);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x[4] = {gelu_tanh(bf16_lo(uu[j][q][0])), gelu_tanh(bf16_hi(uu[j][q][0])),
+                              gelu_tanh(bf16_lo(uu[j][q][1])), gelu_tanh(bf16_hi(uu[j][q][1]))};
+          if constexpr (sizeof(OutT) == 2) put_bf16(j, q, x);
+          else put_f32(j, q, x);
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float x[4];
+          finish4(i, j, q, x);
+          if constexpr (sizeof(OutT) == 2) put_bf16(j, q, x);
+          else put_f32(j, q, x);
+        }
+    }
+    if constexpr (sizeof(OutT) == 2) copy_out(uint16_t{}, i, g.C, g.ldc);
+    else copy_out(float{}, i, g.C, g.ldc);
   }
 }
 
