@@ -580,7 +580,7 @@ __device__ __forceinline__ void wait_stage(int later) {
 }
 
 template <int BM, int BN, int BKT, int S, bool A_KMAJ, bool B_KMAJ, typename OutT, int EPI>
-__global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2) void gemm2_kernel(GemmArgs g) {
   constexpr int NT = 256;
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int FM = WTM / 32, FN = WTN / 32;
@@ -590,10 +590,19 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   // pre-activation tile (32 KB).
   constexpr bool kBias = EPI == NL_EPI_BIAS || EPI == NL_EPI_BIAS_GELU;
   constexpr bool kAux = EPI == NL_EPI_DGELU;
-  constexpr int kExtra = 32768;
-  constexpr int kEpiBytes = kExtra + (kAux ? BM * BN * 2 : kBias ? 1024 : 0);
-  constexpr int kSmem = S * STAGE * 2 > kEpiBytes ? S * STAGE : kEpiBytes / 2;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[kSmem];
+  static_assert(S == 2 || S == 3, "two or three pipeline stages");
+  // Each pipeline stage is its own LDS object: the compiler can then prove that
+  // the DMA filling one stage does not alias the reads of another and does not
+  // make those reads wait for it.
+  __shared__ __attribute__((aligned(16))) uint16_t st0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st1[STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st2[S > 2 ? STAGE : 8];
+  // Epilogue LDS: four 8 KB store slabs (in the stage buffers), the bias
+  // columns (1 KB) and, for the GELU backward, the saved pre-activation tile
+  // (32 KB: the second stage buffer when stages are that large).
+  constexpr bool kAuxInSt1 = kAux && STAGE * 2 >= BM * BN * 2;
+  __shared__ __attribute__((aligned(16))) float sbias_lds[kBias ? 256 : 4];
+  __shared__ __attribute__((aligned(16))) uint16_t aux_lds[kAux && !kAuxInSt1 ? BM * BN : 8];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -676,27 +685,46 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[cur][j], af[cur][i], acc[i][j]);
     }
   };
-  auto issue = [&](int st) {  // DMA of full stage st (0-based within this split)
-    uint16_t* sb = smem + (st % S) * STAGE;
+  auto issue = [&](uint16_t* sb, int st) {  // DMA of full stage st (0-based within this split)
     const int k0 = kbeg + st * BKT;
     da.issue(ra, sb, k0, g.lda, wave);
     db.issue(rb, sb + BM * BKT, k0, g.ldb, wave);
   };
 
-  // prologue: S-1 stages in flight
-#pragma unroll
-  for (int st = 0; st < S - 1; ++st)
-    if (st < nfull) issue(st);
-  for (int kt = 0; kt < nfull; ++kt) {
-    // stage kt has landed once at most min(S-2, nfull-1-kt) later stages are outstanding
+  // S-stage pipeline, unrolled by S so that every buffer is a fixed LDS object.
+  // Step kt: wait until this wave's DMA of stage kt has landed (later stages
+  // may stay in flight), barrier (stage kt complete for all waves, all waves
+  // done with stage kt-1), start the DMA of stage kt+S-1 into the buffer of
+  // stage kt-1, compute stage kt. With three stages the barrier is a bare
+  // s_barrier (a memory clobber for the compiler): __syncthreads would also
+  // wait for the DMA still in flight.
+  auto step = [&](uint16_t* cur, uint16_t* nxt, int kt) {
     wait_stage<IPS, S - 2>(min(S - 2, nfull - 1 - kt));
-    __syncthreads();  // stage kt visible to all waves; all waves are done with stage kt-1
-    if (kt + S - 1 < nfull) issue(kt + S - 1);
-    compute(smem + (kt % S) * STAGE);
+    if constexpr (S == 2) __syncthreads();
+    else asm volatile("s_barrier" ::: "memory");
+    if (kt + S - 1 < nfull) issue(nxt, kt + S - 1);
+    compute(cur);
+  };
+  if (nfull > 0) issue(st0, 0);
+  if (S > 2 && nfull > 1) issue(st1, 1);
+  if constexpr (S == 2) {
+    for (int kt = 0; kt < nfull; kt += 2) {
+      step(st0, st1, kt);
+      if (kt + 1 >= nfull) break;
+      step(st1, st0, kt + 1);
+    }
+  } else {
+    for (int kt = 0; kt < nfull; kt += 3) {
+      step(st0, st2, kt);
+      if (kt + 1 >= nfull) break;
+      step(st1, st0, kt + 1);
+      if (kt + 2 >= nfull) break;
+      step(st2, st1, kt + 2);
+    }
   }
   if (tail) {
     __syncthreads();
-    uint16_t* sb = smem + (nfull % S) * STAGE;
+    uint16_t* sb = (nfull % S) == 0 ? st0 : (nfull % S) == 1 ? st1 : st2;
     const int kt0 = kbeg + nfull * BKT;
     stage_masked<BM, BKT, A_KMAJ, NT>(g.A, g.lda, m0, g.M, kt0, kend, sb, tid);
     stage_masked<BN, BKT, B_KMAJ, NT>(g.B, g.ldb, n0, g.N, kt0, kend, sb + BM * BKT, tid);
@@ -728,15 +756,16 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   // for every earlier store, so loads mixed into the store stream would
   // serialise it. The operand tiles' LDS is free once all waves pass the barrier.
   static_assert((!kBias && !kAux) || (BM == 128 && BN == 128), "the staged epilogue assumes 128 x 128 tiles");
-  uint16_t* const xlds = smem + kExtra / 2;
-  const float* sbias = reinterpret_cast<const float*>(xlds);
+  uint16_t* const xlds = kAuxInSt1 ? st1 : aux_lds;
+  const float* sbias = sbias_lds;
   __syncthreads();
   if constexpr (kBias || kAux) {
     if constexpr (kBias) {
       // bias[n0 .. n0+255] -> 1 KB (only the first 128 are read); clipped at N
       if (wave == 0) {
         const __amdgpu_buffer_rsrc_t rbias = make_rsrc(g.bias, (uint32_t)g.N * 4u);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rbias, (lds_void*)xlds, 16, (uint32_t)(n0 + lane * 4) * 4u, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rbias, (lds_void*)sbias_lds, 16, (uint32_t)(n0 + lane * 4) * 4u, 0, 0,
+                                                 0);
       }
     } else {
       // aux tile [128][128] bf16: row r at r*256 bytes, 16-byte chunk c at slot c ^ (r & 15)
@@ -789,7 +818,9 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
   // 16-byte pieces of a row. Values are finished (scale, bias, GELU') group by
   // group on the way into LDS, which keeps few of them live in VGPRs.
   static_assert(WTN == 64, "the store transpose assumes 64-column wave tiles");
-  uint8_t* wl = reinterpret_cast<uint8_t*>(smem) + wave * 8192;
+  static_assert(STAGE * 2 >= 16384, "two 8 KB slabs per stage buffer");
+  uint8_t* wl = kAuxInSt1 ? reinterpret_cast<uint8_t*>(st0) + wave * 8192
+                          : reinterpret_cast<uint8_t*>(wave < 2 ? st0 : st1) + (wave & 1) * 8192;
   auto finish4 = [&](int i, int j, int q, float x[4]) {
     const int nl = wn * WTN + j * 32 + q * 8 + g4;
     f32x4 b = {0.f, 0.f, 0.f, 0.f};
@@ -893,13 +924,21 @@ __global__ __launch_bounds__(256) void gemm2_kernel(GemmArgs g) {
 // Explicit instantiations: every (layout, output, epilogue) combination the
 // dispatcher can launch gets its host stub emitted. k-stage depth per layout:
 // 64 when both operands are k-major (NT), else 32 (see launch_cfg).
-#define NL_I(AK, BKM, T, E) template __global__ void gemm2_kernel<128, 128, (AK && BKM) ? 64 : 32, 2, AK, BKM, T, E>(GemmArgs);
+#ifndef NL_GEMM_STAGES32
+#define NL_GEMM_STAGES32 2
+#endif
+#define NL_I(AK, BKM, T, E) \
+  template __global__ void gemm2_kernel<128, 128, (AK && BKM) ? 64 : 32, (AK && BKM) ? 2 : NL_GEMM_STAGES32, AK, BKM, T, E>(GemmArgs);
 #define NL_I4(T, E) NL_I(true, false, T, E) NL_I(true, true, T, E) NL_I(false, false, T, E) NL_I(false, true, T, E)
 #define NL_I8(E) NL_I4(float, E) NL_I4(uint16_t, E)
 NL_I8(NL_EPI_NONE)
 NL_I8(NL_EPI_BIAS)
 NL_I8(NL_EPI_BIAS_GELU)
 NL_I8(NL_EPI_DGELU)
+template __global__ void gemm2_kernel<256, 128, 32, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 128, 32, 2, true, false, uint16_t, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 128, 32, 2, false, false, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 128, 32, 2, false, false, uint16_t, NL_EPI_NONE>(GemmArgs);
 #undef NL_I8
 #undef NL_I4
 #undef NL_I
@@ -933,7 +972,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int spli
 
 // Tile configuration and K split of one product (shared by the workspace query).
 struct Plan {
-  int big;     // 1: 256x256 tiles, 0: 128x128
+  int big;     // 1: 256 x 128 tiles (the very large products), 0: 128 x 128
   int tiles;
   int splits;
   int k_chunk;
@@ -941,21 +980,16 @@ struct Plan {
   size_t ws_bytes;
 };
 
-Plan make_plan(int M, int N, int K) {
+Plan make_plan(int opA, int opB, int M, int N, int K, int epi) {
   Plan p;
-  const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-  (void)t256;
-  // 128 x 128 tiles everywhere: measured on MI355X, 256 x 256 tiles (one
-  // workgroup per CU) were no faster on any model shape.
   p.big = 0;
-  const int bm = p.big ? 256 : 128;
-  p.tiles = (int)((int64_t)((M + bm - 1) / bm) * ((N + bm - 1) / bm));
+  p.tiles = (int)((int64_t)((M + 127) / 128) * ((N + 127) / 128));
   p.splits = 1;
   p.k_chunk = K > 0 ? K : 1;
   // skinny outputs with a long reduction (weight gradients, K = tokens): split K
   // until ~640 workgroups are in flight, keeping >= 512 k per split
-  if (p.tiles < 256 && K >= 1024) {
-    int want = (640 + p.tiles - 1) / p.tiles;
+  if ((p.tiles < 256 && K >= 1024) || (p.tiles < 1024 && K >= 16384)) {
+    int want = (p.tiles < 256 ? 640 + p.tiles - 1 : 1024 + p.tiles - 1) / p.tiles;
     int maxs = K / 512;
     int sp = want < maxs ? want : maxs;
     if (sp > 1) {
@@ -965,43 +999,63 @@ Plan make_plan(int M, int N, int K) {
       p.splits = (K + chunk - 1) / chunk;
     }
   }
+  // 256 x 128 tiles (4 waves of 128 x 64) for the largest products whose B is
+  // k-by-n (NN, TN) and that need no fused epilogue: measured on MI355X, they
+  // beat 128 x 128 on the LM head (TN 16384-deep: ~15%), lose on the FFN sizes.
+  if (p.splits == 1 && opB == NL_OP_N && epi == NL_EPI_NONE &&
+      ((opA == NL_OP_T && p.tiles >= 1024) || (opA == NL_OP_N && p.tiles >= 8192))) {
+    p.big = 1;
+    p.tiles = (int)((int64_t)((M + 255) / 256) * ((N + 127) / 128));
+  }
   p.ldw = ((int64_t)N + 7) / 8 * 8;
   p.ws_bytes = p.splits > 1 ? (size_t)p.splits * M * p.ldw * sizeof(float) : 0;
   return p;
 }
 
 template <int BM, int BN, int WM, int WN, bool AK, bool BK_, typename OutT>
-void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
-  g.tiles = p.tiles;
-  g.k_chunk = p.k_chunk;
+void launch_cfg(GemmArgs g, const Plan& plan, hipStream_t st) {
+  Plan p = plan;
   // the v2 kernel addresses operands with 32-bit buffer offsets
-  const int64_t a_ext = (AK ? (int64_t)g.M + BM : (int64_t)g.K + BK) * g.lda * 2;
+  const int64_t a_ext = (AK ? (int64_t)g.M + 2 * BM : (int64_t)g.K + BK) * g.lda * 2;
   const int64_t b_ext = (BK_ ? (int64_t)g.N + BN : (int64_t)g.K + BK) * g.ldb * 2;
   // (the DGELU epilogue also reads its aux tile through a buffer descriptor)
   const int64_t aux_ext = g.epi == NL_EPI_DGELU ? ((int64_t)g.M + BM) * g.ldaux * 2 : 0;
   const bool v2 = WM == 2 && WN == 2 && a_ext < ((int64_t)1 << 31) && b_ext < ((int64_t)1 << 31) &&
                   aux_ext < ((int64_t)1 << 31);
+  if (p.big && !v2) {  // the register-staged kernel only has 128 x 128 tiles
+    p.big = 0;
+    p.tiles = (int)((int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128));
+  }
+  g.tiles = p.tiles;
+  g.k_chunk = p.k_chunk;
   // Pipeline choice measured on MI355X at the model's shapes: with both
   // operands k-major (NT) 64-k stages win; otherwise 32-k stages (32 KB of LDS,
   // more workgroups per CU to cover L2-miss latency) win.
   auto launch2 = [&](int grid) {
+    if constexpr (!BK_) {
+      if (p.big) {
+        hipLaunchKernelGGL((gemm2_kernel<256, 128, 32, 2, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(256), 0, st, g);
+        return;
+      }
+    }
     constexpr int BKT = (AK && BK_) ? 64 : 32;
+    constexpr int NS = (AK && BK_) ? 2 : NL_GEMM_STAGES32;
     // with split K the epilogue runs in the reduction kernel
     const int epi = g.ws ? NL_EPI_NONE : g.epi;
     switch (epi) {
       case NL_EPI_BIAS:
-        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_BIAS>), dim3(grid), dim3(256), 0, st, g);
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, NS, AK, BK_, OutT, NL_EPI_BIAS>), dim3(grid), dim3(256), 0, st, g);
         break;
       case NL_EPI_BIAS_GELU:
-        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_BIAS_GELU>), dim3(grid), dim3(256), 0,
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, NS, AK, BK_, OutT, NL_EPI_BIAS_GELU>), dim3(grid), dim3(256), 0,
                            st, g);
         break;
       case NL_EPI_DGELU:
-        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_DGELU>), dim3(grid), dim3(256), 0, st,
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, NS, AK, BK_, OutT, NL_EPI_DGELU>), dim3(grid), dim3(256), 0, st,
                            g);
         break;
       default:
-        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, 2, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(256), 0, st, g);
+        hipLaunchKernelGGL((gemm2_kernel<128, 128, BKT, NS, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(256), 0, st, g);
     }
   };
   if (p.splits > 1) {
@@ -1041,10 +1095,8 @@ void launch_typed(int opA, int opB, const GemmArgs& g, const Plan& p, hipStream_
 using namespace nl;
 
 extern "C" size_t nl_gemm_ws_bytes(int opA, int opB, int M, int N, int K) {
-  (void)opA;
-  (void)opB;
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return make_plan(M, N, K).ws_bytes;
+  return make_plan(opA, opB, M, N, K, NL_EPI_NONE).ws_bytes;
 }
 
 extern "C" int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
@@ -1092,7 +1144,7 @@ extern "C" int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K
   g.bias = bias;
   g.aux = aux;
   g.ldaux = ldaux;
-  Plan p = make_plan(M, N, K);
+  Plan p = make_plan(opA, opB, M, N, K, epi);
   if (p.splits > 1 && (!ws || ws_bytes < p.ws_bytes || ((uintptr_t)ws & 15) != 0)) {
     // no (usable) workspace: one workgroup per tile over the whole K range
     p.splits = 1;

@@ -157,3 +157,24 @@ def test_gemm_split_k_matches_single_pass_and_is_deterministic(dev, M, N, K):
     cols = np.random.default_rng(1).choice(N, min(N, 32), replace=False)
     ct = torch.from_numpy(cols).to(dev)
     assert rel_l2(_np(split1[:, ct]), ops.gemm(_np(X), _np(dY[:, ct]), "T", "N")) <= 5e-3
+
+
+@pytest.mark.parametrize("opA,M,N,K", [("T", 500, 50257, 200), ("N", 16312, 8192, 72)])
+def test_gemm_tall_tile_path_exact_small_integers(dev, opA, M, N, K):
+    """Products large enough for the 256 x 128 tile path (ragged M, N and K),
+    checked exactly on integer inputs over sampled rows including both edges."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels.gemm import gemm_raw
+
+    tiles128 = ((M + 127) // 128) * ((N + 127) // 128)
+    assert tiles128 >= (1024 if opA == "T" else 8192)       # the dispatcher picks the tall tiles
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-3, 4, (M, K)).astype(np.float32)
+    B = rng.integers(-3, 4, (K, N)).astype(np.float32)
+    As = A.T.copy() if opA == "T" else A
+    C = gemm_raw(_dev_bf16(As, dev), _dev_bf16(B, dev), opA, "N")
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, 130), np.arange(M - 130, M), rng.integers(0, M, 200)]))
+    got = C[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+    assert np.array_equal(got, A[rows] @ B)
