@@ -105,6 +105,35 @@ __device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const 
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
 
+// ---------------------------------------------------------------------------
+// Global -> LDS DMA and transposing LDS reads
+// ---------------------------------------------------------------------------
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Raw buffer resource over [p, p + bytes): loads past the end return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane l lands at lds + 16 l.
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) (other counters unconstrained), n < 64
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// ds_read_b64_tr_b16: lane 16G+i receives element i%4 of the 8 bytes addressed by
+// lanes 16G+4e+i/4, e = 0..3 (a 4x4 transpose of 16-bit elements per 16 lanes).
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* lds) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)lds));
+}
+
 // 8x8 transpose of 16-bit elements held as 8 rows x 4 dwords.
 // in[r] holds row r: dword j = (col 2j, col 2j+1). out[c] holds column c:
 // dword j = (row 2j, row 2j+1). 32 v_perm_b32.

@@ -115,6 +115,66 @@ __device__ __forceinline__ void zero(f32x16& a) {
   for (int r = 0; r < 16; ++r) a[r] = 0.f;
 }
 
+// ---- DMA path: 64 x 64 bf16 tiles filled straight from global memory into LDS
+// (buffer_load ... lds): 128-byte rows of eight 16-byte chunks, chunk c of row k
+// at slot c ^ swz(k). The one swizzle serves both ways a tile is read:
+//   * 16-byte reads of one chunk down 16 consecutive rows (MFMA fragments along
+//     a row): the 8 even rows get 8 distinct slots, the odd rows sit in the
+//     other half of the banks;
+//   * ds_read_b64_tr_b16 over 4 consecutive rows x 4 chunks per 32 lanes
+//     (MFMA fragments down a column): rows k and k+2 map the 4-chunk group to
+//     disjoint slots.
+__device__ __forceinline__ int swz(int k) { return (((k >> 1) & 1) << 2) | ((k >> 2) & 3); }
+// Tiles read one way only (the forward's K along rows, V down columns) use the
+// cheaper single-purpose swizzles (fewer distinct fragment addresses to keep).
+__device__ __forceinline__ int swz_rows(int k) { return (k ^ (k >> 3)) & 7; }
+__device__ __forceinline__ int swz_cols(int k) { return ((k >> 1) & 1) << 2; }
+enum Swz { kBoth, kAlongRows, kDownCols };
+template <int W>
+__device__ __forceinline__ int swz_of(int k) {
+  if constexpr (W == kAlongRows) return swz_rows(k);
+  else if constexpr (W == kDownCols) return swz_cols(k);
+  else return swz(k);
+}
+
+// DMA rows row0 .. row0+63 (row stride ld elements) of the buffer into a tile:
+// 4 waves x 2 instructions x 64 lanes x 16 bytes. Rows past the buffer's end
+// read as zero.
+template <int W = kBoth>
+__device__ __forceinline__ void dma_tile(__amdgpu_buffer_rsrc_t rs, uint16_t* lds, int row0, int64_t ld, int wave,
+                                         int lane) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int blk = i * 4 + wave;           // 1 KB of the tile = 8 rows
+    const int u = blk * 64 + lane;          // destination chunk
+    const int r = u >> 3, slot = u & 7;
+    const int c = slot ^ swz_of<W>(r);
+    dma16(rs, lds + blk * 512, (uint32_t)(((int64_t)(row0 + r) * ld + c * 8) * 2), 0);
+  }
+}
+// 8 consecutive columns c*8.. of row r
+template <int W = kBoth>
+__device__ __forceinline__ bf16x8 frag_R(const uint16_t* t, int r, int c) {
+  return as_bf16x8(*reinterpret_cast<const u32x4*>(t + r * 64 + ((c ^ swz_of<W>(r)) << 3)));
+}
+// MFMA operand down the columns of a tile [k][mn]: lane (mn = mnb + lane%32, g = lane/32) gets
+// t[k][mn] for k = kb + {4g..4g+3, 8+4g..8+4g+3} -- the permuted k order that
+// matches pack_frag of a 32x32 accumulator.
+template <int W = kBoth>
+__device__ __forceinline__ bf16x8 frag_T(const uint16_t* t, int mnb, int kb, int lane) {
+  const int G = lane >> 4, j = lane & 15;
+  const int mn = mnb + 16 * (G & 1) + 4 * (j & 3);
+  const int k0 = kb + 4 * (G >> 1) + (j >> 2);
+  const int k1 = k0 + 8;
+  const u32x2 lo = ds_read_tr16(t + k0 * 64 + (((mn >> 3) ^ swz_of<W>(k0)) << 3) + (mn & 7));
+  const u32x2 hi = ds_read_tr16(t + k1 * 64 + (((mn >> 3) ^ swz_of<W>(k1)) << 3) + (mn & 7));
+  return as_bf16x8(u32x4{lo[0], lo[1], hi[0], hi[1]});
+}
+// Buffer resource over rows 0 .. S-1 of one head (row stride ld, 64 columns).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t head_rsrc(const uint16_t* p, int S, int64_t ld) {
+  return make_rsrc(p, (uint32_t)((((int64_t)(S - 1)) * ld + 64) * 2));
+}
+
 struct Op {
   const uint16_t* p;
   nl_attn_stride s;
@@ -155,14 +215,18 @@ __device__ __forceinline__ void store_row64(uint16_t* rowp, const f32x16 acc[2],
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void flash_fwd_kernel(FwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[2][kBlk * kD];
+__global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
+  // double-buffered K and V blocks; every buffer its own
+  // LDS object so the DMA of block kb+1 never makes the reads of block kb wait
+  __shared__ __attribute__((aligned(16))) uint16_t sK0[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sK1[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sV1[kBlk * kD];
   const int S = a.S;
   const int nqt = (S + kRows - 1) / kRows;
   const int qt = nqt - 1 - (int)blockIdx.x;  // heaviest (latest) query tiles first
   const int h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int qw0 = qt * kRows + wave * 32;  // first query of this wave
   const int q = qw0 + l32;                 // this lane's query
@@ -178,83 +242,86 @@ __global__ __launch_bounds__(kThreads) void flash_fwd_kernel(FwdArgs a) {
   const int kend_wg = a.causal ? min(S, qt * kRows + kRows) : S;
   const int kend_w = a.causal ? min(S, qw0 + 32) : S;
   const int nkb = (kend_wg + kBlk - 1) / kBlk;
+  const __amdgpu_buffer_rsrc_t rk = head_rsrc(a.k.at(b, h, 0), S, a.k.s.row);
+  const __amdgpu_buffer_rsrc_t rv = head_rsrc(a.v.at(b, h, 0), S, a.v.s.row);
+  auto issue = [&](uint16_t* sk, uint16_t* sv, int kb) {
+    dma_tile<kAlongRows>(rk, sk, kb * kBlk, a.k.s.row, wave, lane);
+    dma_tile<kDownCols>(rv, sv, kb * kBlk, a.v.s.row, wave, lane);
+  };
 
-  float m = -INFINITY, l = 0.f;
+  const float c = a.scale_log2;  // scores are kept raw; exp2 arguments are c * s - m
+  float m = -INFINITY, l = 0.f;  // running max (scaled, log2 units) and this lane's partial sum
   f32x16 o[2];
   zero(o[0]);
   zero(o[1]);
 
-  RowTile tk;
-  TransTile tv;
-  tk.load(a.k.at(b, h, 0), a.k.s.row, min(kBlk, S), tid);
-  tv.load(a.v.at(b, h, 0), a.v.s.row, min(kBlk, S), tid);
-  tk.store(sK[0], tid);
-  tv.store(sVt[0], tid);
-  __syncthreads();
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
+  auto compute = [&](const uint16_t* sk, const uint16_t* sv, int kb) {
     const int k0 = kb * kBlk;
-    const bool more = kb + 1 < nkb;
-    if (more) {
-      tk.load(a.k.at(b, h, k0 + kBlk), a.k.s.row, min(kBlk, S - k0 - kBlk), tid);
-      tv.load(a.v.at(b, h, k0 + kBlk), a.v.s.row, min(kBlk, S - k0 - kBlk), tid);
+    if (k0 >= kend_w) return;  // every query of this wave precedes the block
+    // S^T (keys x queries): lane (query, g) holds keys k0 + kt*32 + 8(r/4) + 4g + r%4
+    f32x16 s[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      zero(s[kt]);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) s[kt] = mfma32(frag_R<kAlongRows>(sk, kt * 32 + l32, ks * 2 + g), qf[ks], s[kt]);
     }
-    if (k0 < kend_w) {
-      f32x16 s[2];
+    const bool need_mask = (a.causal && k0 + kBlk - 1 > qw0) || (k0 + kBlk > S);
+    float bm = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        zero(s[kt]);
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) s[kt] = mfma32(row_frag(sK[buf], kt * 32 + l32, ks * 2 + g), qf[ks], s[kt]);
+      for (int r = 0; r < 16; ++r) {
+        float x = s[kt][r];
+        if (need_mask) {
+          const int key = k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (key >= S || (a.causal && key > q)) x = -INFINITY;
+        }
+        s[kt][r] = x;
+        bm = fmaxf(bm, x);
       }
-      const bool need_mask = (a.causal && k0 + kBlk - 1 > qw0) || (k0 + kBlk > S);
-      float bm = -INFINITY;
+    bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
+    const float mn = fmaxf(m, bm * c);
+    const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
+    const float nmn = (mn == -INFINITY) ? 0.f : -mn;
+    float rs = 0.f;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = s[kt][r] * a.scale_log2;
-          if (need_mask) {
-            const int key = k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= S || (a.causal && key > q)) x = -INFINITY;
-          }
-          s[kt][r] = x;
-          bm = fmaxf(bm, x);
-        }
-      bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-      const float mn = fmaxf(m, bm);
-      const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
-      float rs = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(__builtin_fmaf(s[kt][r], c, nmn));  // -inf -> 0
+        s[kt][r] = p;
+        rs += p;
+      }
+    l = __builtin_fmaf(l, alpha, rs);
+    m = mn;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+    for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = (mn == -INFINITY) ? 0.f : fast_exp2(s[kt][r] - mn);
-          s[kt][r] = p;
-          rs += p;
-        }
-      l = l * alpha + rs;
-      m = mn;
+      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    // O^T (d x queries) += V^T P^T, P straight from the registers
 #pragma unroll
-      for (int dt = 0; dt < 2; ++dt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+      for (int hh = 0; hh < 2; ++hh) {
+        const bf16x8 pf = pack_frag(s[kt], hh);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const bf16x8 pf = pack_frag(s[kt], hh);
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
-            o[dt] = mfma32(trans_frag(sVt[buf], dt * 32 + l32, kt * 32 + hh * 16, g), pf, o[dt]);
-        }
-    }
-    if (more) {
-      tk.store(sK[buf ^ 1], tid);
-      tv.store(sVt[buf ^ 1], tid);
-    }
+        for (int dt = 0; dt < 2; ++dt)
+          o[dt] = mfma32(frag_T<kDownCols>(sv, dt * 32, kt * 32 + hh * 16, lane), pf, o[dt]);
+      }
+  };
+
+  if (nkb > 0) issue(sK0, sV0, 0);
+  for (int kb = 0; kb < nkb; kb += 2) {
+    wait_vm<0>();
     __syncthreads();
+    if (kb + 1 < nkb) issue(sK1, sV1, kb + 1);
+    compute(sK0, sV0, kb);
+    if (kb + 1 >= nkb) break;
+    wait_vm<0>();
+    __syncthreads();
+    if (kb + 2 < nkb) issue(sK0, sV0, kb + 2);
+    compute(sK1, sV1, kb + 1);
   }
 
   const float lt = l + __shfl_xor(l, 32, kWave);
@@ -304,18 +371,24 @@ struct BwdArgs {
 };
 
 // ---------------------------------------------------------------------------
-// dK, dV: workgroup = 128 keys, streams 64-query blocks from the diagonal on
+// dK, dV: workgroup = 128 keys, streams 64-query blocks from the diagonal on.
+// Per block the Q and dO tiles (and L, D) arrive by DMA; each tile is read both
+// along rows (S = Q K^T, dP = dO V^T) and down columns (dV += dO^T P,
+// dK += Q^T dS) from the one LDS copy.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void flash_bwd_dkdv_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sQ[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) uint16_t sQt[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) uint16_t sdO[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) uint16_t sdOt[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) float sL[2][kBlk], sDv[2][kBlk];
+__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sQ0[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sQ1[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sO0[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sO1[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) float sL0[kBlk];
+  __shared__ __attribute__((aligned(16))) float sL1[kBlk];
+  __shared__ __attribute__((aligned(16))) float sD0[kBlk];
+  __shared__ __attribute__((aligned(16))) float sD1[kBlk];
   const int S = a.S;
   const int kt_idx = blockIdx.x;  // low key tiles see the most queries: launched first
   const int h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int kw0 = kt_idx * kRows + wave * 32;
   const int key = kw0 + l32;
@@ -340,87 +413,78 @@ __global__ __launch_bounds__(kThreads) void flash_bwd_dkdv_kernel(BwdArgs a) {
 
   const int qstart = a.causal ? (kt_idx * kRows) / kBlk * kBlk : 0;
   const int nqb = (S - qstart + kBlk - 1) / kBlk;
-
-  RowTile tq, tdo;
-  TransTile tqt, tdot;
-  float lv = 0.f, dv_ = 0.f;
-  auto load_block = [&](int q0) {
-    const int nv = min(kBlk, S - q0);
-    tq.load(a.q.at(b, h, q0), a.q.s.row, nv, tid);
-    tqt.load(a.q.at(b, h, q0), a.q.s.row, nv, tid);
-    tdo.load(a.dout.at(b, h, q0), a.dout.s.row, nv, tid);
-    tdot.load(a.dout.at(b, h, q0), a.dout.s.row, nv, tid);
-    if (tid < kBlk) {
-      lv = (tid < nv) ? a.L[lbase + q0 + tid] * kLog2e : INFINITY;  // +inf -> P = 0 for padding rows
-      dv_ = (tid < nv) ? a.D[lbase + q0 + tid] : 0.f;
-    }
-  };
-  auto store_block = [&](int buf) {
-    tq.store(sQ[buf], tid);
-    tqt.store(sQt[buf], tid);
-    tdo.store(sdO[buf], tid);
-    tdot.store(sdOt[buf], tid);
-    if (tid < kBlk) {
-      sL[buf][tid] = lv;
-      sDv[buf][tid] = dv_;
-    }
-  };
-  if (nqb > 0) {
-    load_block(qstart);
-    store_block(0);
-  }
-  __syncthreads();
-
-  for (int qb = 0; qb < nqb; ++qb) {
-    const int buf = qb & 1;
+  const __amdgpu_buffer_rsrc_t rq = head_rsrc(a.q.at(b, h, 0), S, a.q.s.row);
+  const __amdgpu_buffer_rsrc_t ro = head_rsrc(a.dout.at(b, h, 0), S, a.dout.s.row);
+  const __amdgpu_buffer_rsrc_t rl = make_rsrc(a.L + lbase, (uint32_t)S * 4u);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(a.D + lbase, (uint32_t)S * 4u);
+  auto issue = [&](uint16_t* sq, uint16_t* so, float* sl, float* sd, int qb) {
     const int q0 = qstart + qb * kBlk;
-    const bool more = qb + 1 < nqb;
-    if (more) load_block(q0 + kBlk);
+    dma_tile(rq, sq, q0, a.q.s.row, wave, lane);
+    dma_tile(ro, so, q0, a.dout.s.row, wave, lane);
+    if (lane < 16) {  // 64 floats of L (wave 0) and of D (wave 1); rows past S read zero
+      if (wave == 0) dma16(rl, sl, (uint32_t)(q0 + lane * 4) * 4u, 0);
+      if (wave == 1) dma16(rd, sd, (uint32_t)(q0 + lane * 4) * 4u, 0);
+    }
+  };
+  const float c = a.scale_log2;
+
+  auto compute = [&](const uint16_t* sq, const uint16_t* so, const float* sl, const float* sd, int qb) {
+    const int q0 = qstart + qb * kBlk;
     // this wave's keys see queries >= kw0 only (causal)
-    if (!a.causal || q0 + kBlk - 1 >= kw0) {
-      const bool need_mask = (a.causal && q0 < kw0 + 31) || (q0 + kBlk > S);
+    if (a.causal && q0 + kBlk - 1 < kw0) return;
+    const bool need_mask = (a.causal && q0 < kw0 + 31) || (q0 + kBlk > S);
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
-        f32x16 s, dp;
-        zero(s);
-        zero(dp);
+    for (int qt = 0; qt < 2; ++qt) {
+      f32x16 s, dp;
+      zero(s);
+      zero(dp);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          s = mfma32(row_frag(sQ[buf], qt * 32 + l32, ks * 2 + g), kf[ks], s);
-          dp = mfma32(row_frag(sdO[buf], qt * 32 + l32, ks * 2 + g), vf[ks], dp);
-        }
-        // lane (key, g) holds query rows qt*32 + 8qq + 4g + t
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma32(frag_R(sq, qt * 32 + l32, ks * 2 + g), kf[ks], s);
+        dp = mfma32(frag_R(so, qt * 32 + l32, ks * 2 + g), vf[ks], dp);
+      }
+      // lane (key, g) holds query rows qt*32 + 8qq + 4g + t
 #pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int qr = qt * 32 + qq * 8 + 4 * g;
-          const f32x4 L4 = *reinterpret_cast<const f32x4*>(&sL[buf][qr]);
-          const f32x4 D4 = *reinterpret_cast<const f32x4*>(&sDv[buf][qr]);
+      for (int qq = 0; qq < 4; ++qq) {
+        const int qr = qt * 32 + qq * 8 + 4 * g;
+        const f32x4 L4 = *reinterpret_cast<const f32x4*>(sl + qr);
+        const f32x4 D4 = *reinterpret_cast<const f32x4*>(sd + qr);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) {
-            const int r = 4 * qq + t;
-            float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -L4[t]));
-            if (need_mask) {
-              const int qi = q0 + qr + t;
-              if (qi >= S || (a.causal && qi < key)) p = 0.f;
-            }
-            s[r] = p;
-            dp[r] = p * (dp[r] - D4[t]);
+        for (int t = 0; t < 4; ++t) {
+          const int r = 4 * qq + t;
+          float p = fast_exp2(__builtin_fmaf(s[r], c, -L4[t] * kLog2e));
+          if (need_mask) {
+            const int qi = q0 + qr + t;
+            if (qi >= S || (a.causal && qi < key)) p = 0.f;
           }
+          s[r] = p;
+          dp[r] = p * (dp[r] - D4[t]);
         }
+      }
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const bf16x8 pf = pack_frag(s, hh);
-          const bf16x8 dsf = pack_frag(dp, hh);
+      for (int hh = 0; hh < 2; ++hh) {
+        const bf16x8 pf = pack_frag(s, hh);
+        const bf16x8 dsf = pack_frag(dp, hh);
 #pragma unroll
-          for (int dt = 0; dt < 2; ++dt) {
-            dv[dt] = mfma32(trans_frag(sdOt[buf], dt * 32 + l32, qt * 32 + hh * 16, g), pf, dv[dt]);
-            dk[dt] = mfma32(trans_frag(sQt[buf], dt * 32 + l32, qt * 32 + hh * 16, g), dsf, dk[dt]);
-          }
+        for (int dt = 0; dt < 2; ++dt) {
+          dv[dt] = mfma32(frag_T(so, dt * 32, qt * 32 + hh * 16, lane), pf, dv[dt]);
+          dk[dt] = mfma32(frag_T(sq, dt * 32, qt * 32 + hh * 16, lane), dsf, dk[dt]);
         }
       }
     }
-    if (more) store_block(buf ^ 1);
+  };
+
+  if (nqb > 0) issue(sQ0, sO0, sL0, sD0, 0);
+  for (int qb = 0; qb < nqb; qb += 2) {
+    wait_vm<0>();
     __syncthreads();
+    if (qb + 1 < nqb) issue(sQ1, sO1, sL1, sD1, qb + 1);
+    compute(sQ0, sO0, sL0, sD0, qb);
+    if (qb + 1 >= nqb) break;
+    wait_vm<0>();
+    __syncthreads();
+    if (qb + 2 < nqb) issue(sQ0, sO0, sL0, sD0, qb + 2);
+    compute(sQ1, sO1, sL1, sD1, qb + 1);
   }
   if (kvalid) {
     store_row64(a.dk.at(b, h, key), dk, a.scale, g);
@@ -429,17 +493,19 @@ __global__ __launch_bounds__(kThreads) void flash_bwd_dkdv_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ: workgroup = 128 queries, streams 64-key blocks up to the diagonal
+// dQ: workgroup = 128 queries, streams 64-key blocks up to the diagonal; the
+// K tile is read along rows (S) and down columns (dQ += dS K).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads) void flash_bwd_dq_kernel(BwdArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sK[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[2][kBlk * kD];
-  __shared__ __attribute__((aligned(16))) uint16_t sKt[2][kBlk * kD];
+__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(BwdArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t sK0[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sK1[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[kBlk * kD];
+  __shared__ __attribute__((aligned(16))) uint16_t sV1[kBlk * kD];
   const int S = a.S;
   const int nqt = (S + kRows - 1) / kRows;
   const int qt = nqt - 1 - (int)blockIdx.x;
   const int h = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int qw0 = qt * kRows + wave * 32;
   const int q = qw0 + l32;
@@ -456,73 +522,67 @@ __global__ __launch_bounds__(kThreads) void flash_bwd_dq_kernel(BwdArgs a) {
       df[ks] = global_frag(dp + ks * 16 + g * 8, qvalid);
     }
   }
-  const float Lq = qvalid ? a.L[lbase + q] * kLog2e : INFINITY;
+  const float c = a.scale_log2;
+  const float nLq = qvalid ? -a.L[lbase + q] * kLog2e : -INFINITY;
   const float Dq = qvalid ? a.D[lbase + q] : 0.f;
 
   const int kend_wg = a.causal ? min(S, qt * kRows + kRows) : S;
   const int kend_w = a.causal ? min(S, qw0 + 32) : S;
   const int nkb = (kend_wg + kBlk - 1) / kBlk;
+  const __amdgpu_buffer_rsrc_t rk = head_rsrc(a.k.at(b, h, 0), S, a.k.s.row);
+  const __amdgpu_buffer_rsrc_t rv = head_rsrc(a.v.at(b, h, 0), S, a.v.s.row);
+  auto issue = [&](uint16_t* sk, uint16_t* sv, int kb) {
+    dma_tile(rk, sk, kb * kBlk, a.k.s.row, wave, lane);
+    dma_tile(rv, sv, kb * kBlk, a.v.s.row, wave, lane);
+  };
 
   f32x16 dq[2];
   zero(dq[0]);
   zero(dq[1]);
 
-  RowTile tk, tv;
-  TransTile tkt;
-  tk.load(a.k.at(b, h, 0), a.k.s.row, min(kBlk, S), tid);
-  tv.load(a.v.at(b, h, 0), a.v.s.row, min(kBlk, S), tid);
-  tkt.load(a.k.at(b, h, 0), a.k.s.row, min(kBlk, S), tid);
-  tk.store(sK[0], tid);
-  tv.store(sV[0], tid);
-  tkt.store(sKt[0], tid);
-  __syncthreads();
-
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int buf = kb & 1;
+  auto compute = [&](const uint16_t* sk, const uint16_t* sv, int kb) {
     const int k0 = kb * kBlk;
-    const bool more = kb + 1 < nkb;
-    if (more) {
-      const int nv = min(kBlk, S - k0 - kBlk);
-      tk.load(a.k.at(b, h, k0 + kBlk), a.k.s.row, nv, tid);
-      tv.load(a.v.at(b, h, k0 + kBlk), a.v.s.row, nv, tid);
-      tkt.load(a.k.at(b, h, k0 + kBlk), a.k.s.row, nv, tid);
-    }
-    if (k0 < kend_w) {
-      const bool need_mask = (a.causal && k0 + kBlk - 1 > qw0) || (k0 + kBlk > S);
+    if (k0 >= kend_w) return;
+    const bool need_mask = (a.causal && k0 + kBlk - 1 > qw0) || (k0 + kBlk > S);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        f32x16 s, dp;
-        zero(s);
-        zero(dp);
+    for (int kt = 0; kt < 2; ++kt) {
+      f32x16 s, dp;
+      zero(s);
+      zero(dp);
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          s = mfma32(row_frag(sK[buf], kt * 32 + l32, ks * 2 + g), qf[ks], s);
-          dp = mfma32(row_frag(sV[buf], kt * 32 + l32, ks * 2 + g), df[ks], dp);
+      for (int ks = 0; ks < 4; ++ks) {
+        s = mfma32(frag_R(sk, kt * 32 + l32, ks * 2 + g), qf[ks], s);
+        dp = mfma32(frag_R(sv, kt * 32 + l32, ks * 2 + g), df[ks], dp);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = fast_exp2(__builtin_fmaf(s[r], c, nLq));
+        if (need_mask) {
+          const int kk = k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (kk >= S || (a.causal && kk > q)) p = 0.f;
         }
+        dp[r] = p * (dp[r] - Dq);
+      }
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float p = fast_exp2(__builtin_fmaf(s[r], a.scale_log2, -Lq));
-          if (need_mask) {
-            const int key = k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (key >= S || (a.causal && key > q)) p = 0.f;
-          }
-          dp[r] = p * (dp[r] - Dq);
-        }
+      for (int hh = 0; hh < 2; ++hh) {
+        const bf16x8 dsf = pack_frag(dp, hh);
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const bf16x8 dsf = pack_frag(dp, hh);
-#pragma unroll
-          for (int dt = 0; dt < 2; ++dt)
-            dq[dt] = mfma32(trans_frag(sKt[buf], dt * 32 + l32, kt * 32 + hh * 16, g), dsf, dq[dt]);
-        }
+        for (int dt = 0; dt < 2; ++dt) dq[dt] = mfma32(frag_T(sk, dt * 32, kt * 32 + hh * 16, lane), dsf, dq[dt]);
       }
     }
-    if (more) {
-      tk.store(sK[buf ^ 1], tid);
-      tv.store(sV[buf ^ 1], tid);
-      tkt.store(sKt[buf ^ 1], tid);
-    }
+  };
+
+  if (nkb > 0) issue(sK0, sV0, 0);
+  for (int kb = 0; kb < nkb; kb += 2) {
+    wait_vm<0>();
     __syncthreads();
+    if (kb + 1 < nkb) issue(sK1, sV1, kb + 1);
+    compute(sK0, sV0, kb);
+    if (kb + 1 >= nkb) break;
+    wait_vm<0>();
+    __syncthreads();
+    if (kb + 2 < nkb) issue(sK0, sV0, kb + 2);
+    compute(sK1, sV1, kb + 1);
   }
   if (qvalid) store_row64(a.dq.at(b, h, q), dq, a.scale, g);
 }
@@ -531,6 +591,8 @@ __global__ __launch_bounds__(kThreads) void flash_bwd_dq_kernel(BwdArgs a) {
 // host-side validation
 // ---------------------------------------------------------------------------
 bool stride_ok(const nl_attn_stride& s) { return ((s.batch | s.head | s.row) & 7) == 0 && s.row >= 64; }
+// the DMA path addresses one head's rows with 32-bit byte offsets
+bool extent_ok(int S, const nl_attn_stride& s) { return ((int64_t)S * s.row + 64) * 2 < ((int64_t)1 << 31); }
 
 int check_common(int B, int H, int S, int d, int causal) {
   if (B < 0 || H < 0 || S < 0) return nl_set_error(NL_EINVAL, "flash: negative dimension");
@@ -569,6 +631,8 @@ extern "C" int nl_flash_attention_fwd(void* stream, int batch, int heads, int se
   NL_TRY(check_op(V, sv, "V"));
   NL_TRY(check_op(O, so, "O"));
   if (!L) return nl_set_error(NL_EINVAL, "flash: null L");
+  if (!extent_ok(seq, sk) || !extent_ok(seq, sv))
+    return nl_set_error(NL_EUNSUPPORTED, "flash: one head's K or V spans 2 GB or more");
   FwdArgs a;
   a.S = seq;
   a.causal = causal;
@@ -612,6 +676,8 @@ static int fill_bwd(BwdArgs& a, int seq, int causal, float scale, const nl_bf16*
   NL_TRY(check_op(V, sv, "V"));
   NL_TRY(check_op(dO, sdo, "dO"));
   if (!L || !D) return nl_set_error(NL_EINVAL, "flash: null L or D");
+  if (!extent_ok(seq, sq) || !extent_ok(seq, sk) || !extent_ok(seq, sv) || !extent_ok(seq, sdo))
+    return nl_set_error(NL_EUNSUPPORTED, "flash: one head's Q, K, V or dO spans 2 GB or more");
   a.S = seq;
   a.causal = causal;
   a.scale = scale;

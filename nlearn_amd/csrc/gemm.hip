@@ -447,14 +447,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 //   * A ragged K tail (K % 64 != 0) is staged once through registers with
 //     element masks into the same layouts.
 // ===========================================================================
-typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kNW = 4;  // waves per workgroup (2 x 2)
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
 
 // K-major tiles keep CH = BKT/8 16-byte chunks per row; chunk kc of row r sits
 // at slot kc ^ kswz(r). Eight consecutive rows at one chunk (a fragment read)
@@ -552,21 +547,13 @@ struct Frag {
       const int kc = ks * 2 + (lane >> 5);
       return as_bf16x8(*reinterpret_cast<const u32x4*>(tile + off[0] + ((kc ^ sw) << 3)));
     } else {
-      typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
       const uint16_t* t = tile + ks * 16 * ROWS;
-      const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off[0]));
-      const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(t + off[1]));
-      u32x2 a = __builtin_bit_cast(u32x2, lo), b = __builtin_bit_cast(u32x2, hi);
+      const u32x2 a = ds_read_tr16(t + off[0]), b = ds_read_tr16(t + off[1]);
       return as_bf16x8(u32x4{a[0], a[1], b[0], b[1]});
     }
   }
 };
 
-// s_waitcnt vmcnt(n) (other counters unconstrained), n < 64
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // wait until at most `later` stages (IPS DMA ops each) of this wave are outstanding
 template <int IPS, int MAXL>
