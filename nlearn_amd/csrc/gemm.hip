@@ -448,9 +448,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 //     element masks into the same layouts.
 // ===========================================================================
 
-constexpr int kNW = 4;  // waves per workgroup (2 x 2)
-
-
 // K-major tiles keep CH = BKT/8 16-byte chunks per row; chunk kc of row r sits
 // at slot kc ^ kswz(r). Eight consecutive rows at one chunk (a fragment read)
 // land on distinct banks for CH = 8 and CH = 4.
@@ -460,22 +457,23 @@ __device__ __forceinline__ int kswz(int r) {
   else return (r >> 1) & 3;
 }
 
-// Per-lane DMA offsets of one ROWS x BKT operand tile.
-template <int ROWS, int BKT, bool KMAJ>
+// Per-lane DMA offsets of one ROWS x BKT operand tile filled by NW waves.
+template <int ROWS, int BKT, bool KMAJ, int NW>
 struct Dma {
   static constexpr int CH = BKT / 8;
-  static constexpr int INSTR = ROWS * BKT / 8 / 64 / kNW;  // per wave per stage
+  static constexpr int INSTR = ROWS * BKT / 8 / 64 / NW;  // per wave per stage
+  static_assert(INSTR >= 1 && INSTR * 64 * NW * 8 == ROWS * BKT, "a stage splits into whole DMA instructions");
   uint32_t voff[INSTR];  // bytes from the operand base for k0 = 0
   __device__ __forceinline__ void init(int row0, int64_t ld, int wave, int lane) {
 #pragma unroll
     for (int i = 0; i < INSTR; ++i) {
       if constexpr (KMAJ) {
-        const int r = (i * kNW + wave) * (64 / CH) + lane / CH;
+        const int r = (i * NW + wave) * (64 / CH) + lane / CH;
         const int kc = (lane % CH) ^ kswz<CH>(r);
         voff[i] = (uint32_t)(((int64_t)(row0 + r) * ld + kc * 8) * 2);
       } else {
         constexpr int CPR = ROWS / 8, RPI = 64 / CPR;
-        const int k = (i * kNW + wave) * RPI + lane / CPR;
+        const int k = (i * NW + wave) * RPI + lane / CPR;
         const int c = (lane % CPR) ^ ((2 * k) & 15);
         voff[i] = (uint32_t)(((int64_t)k * ld + row0 + c * 8) * 2);
       }
@@ -486,7 +484,7 @@ struct Dma {
     const uint32_t soff = KMAJ ? (uint32_t)(k0 * 2) : (uint32_t)((int64_t)k0 * ld * 2);
 #pragma unroll
     for (int i = 0; i < INSTR; ++i) {
-      const int base_elems = (i * kNW + wave) * 512;  // each instruction fills 64 x 16 bytes
+      const int base_elems = (i * NW + wave) * 512;  // each instruction fills 64 x 16 bytes
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(lds + base_elems), 16, voff[i], soff, 0, 0);
     }
   }
@@ -555,6 +553,30 @@ struct Frag {
 };
 
 
+// Instruction order of one LDS stage for the scheduler: the first k16 step's R
+// fragment reads, then each of the NM MFMAs of step ks followed by its share of
+// step ks+1's reads, so LDS latency hides behind the MFMAs in flight (left to
+// itself the compiler reuses one register set: read, wait, 4 MFMAs, read, ...).
+template <int M, int NM, int R>
+__device__ __forceinline__ void sched_ks() {
+  if constexpr (M < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+    constexpr int lo = M * R / NM, hi = (M + 1) * R / NM;
+    if constexpr (hi > lo) __builtin_amdgcn_sched_group_barrier(0x100, hi - lo, 0);  // ds_reads
+    sched_ks<M + 1, NM, R>();
+  }
+}
+template <int R, int NM, int KS, int KK = 0>
+__device__ __forceinline__ void sched_stage() {
+  if constexpr (KK == 0) __builtin_amdgcn_sched_group_barrier(0x100, R, 0);
+  if constexpr (KK + 1 < KS) {
+    sched_ks<0, NM, R>();
+    sched_stage<R, NM, KS, KK + 1>();
+  } else {
+    __builtin_amdgcn_sched_group_barrier(0x008, NM, 0);
+  }
+}
+
 // wait until at most `later` stages (IPS DMA ops each) of this wave are outstanding
 template <int IPS, int MAXL>
 __device__ __forceinline__ void wait_stage(int later) {
@@ -567,9 +589,16 @@ __device__ __forceinline__ void wait_stage(int later) {
 }
 
 template <int BM, int BN, int BKT, int S, bool A_KMAJ, bool B_KMAJ, typename OutT, int EPI>
-__global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2) void gemm2_kernel(GemmArgs g) {
-  constexpr int NT = 256;
-  constexpr int WTM = BM / 2, WTN = BN / 2;
+__global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
+                             (BM * BN >= 65536) ? 1 : (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2) void gemm2_kernel(GemmArgs g) {
+  // 256 x 256 tiles run 8 waves (2 x 4), the others 4 (2 x 2); every wave
+  // owns a WTM x 64 block of the tile.
+  constexpr bool kHuge = BM * BN >= 65536;
+  constexpr int NWV = kHuge ? 8 : 4;
+  constexpr int NT = 64 * NWV;
+  constexpr int WNW = BN / 64, WMW = NWV / WNW;
+  static_assert(WNW * WMW == NWV, "wave layout");
+  constexpr int WTM = BM / WMW, WTN = 64;
   constexpr int FM = WTM / 32, FN = WTN / 32;
   constexpr int STAGE = (BM + BN) * BKT;  // elements per stage
   // After the K loop the same LDS holds the epilogue: four 8 KB store slabs at
@@ -594,7 +623,7 @@ __global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2)
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WNW, wn = wave % WNW;
 
   int bid = blockIdx.x;
   {
@@ -628,11 +657,11 @@ __global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2)
                                                 : (int64_t)(g.K - 1) * g.ldb + g.N) * 2) + 15) & ~(int64_t)15);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, a_bytes);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, b_bytes);
-  Dma<BM, BKT, A_KMAJ> da;
-  Dma<BN, BKT, B_KMAJ> db;
+  Dma<BM, BKT, A_KMAJ, NWV> da;
+  Dma<BN, BKT, B_KMAJ, NWV> db;
   da.init(m0, g.lda, wave, lane);
   db.init(n0, g.ldb, wave, lane);
-  constexpr int IPS = Dma<BM, BKT, A_KMAJ>::INSTR + Dma<BN, BKT, B_KMAJ>::INSTR;  // DMA ops per stage per wave
+  constexpr int IPS = Dma<BM, BKT, A_KMAJ, NWV>::INSTR + Dma<BN, BKT, B_KMAJ, NWV>::INSTR;  // DMA ops per stage per wave
 
   Frag<BM, BKT, A_KMAJ> fa[FM];
   Frag<BN, BKT, B_KMAJ> fb[FN];
@@ -670,6 +699,11 @@ __global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2)
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[cur][j], af[cur][i], acc[i][j]);
+    }
+    if constexpr (kHuge) {
+      // ds_read instructions per k16 step: one per k-major fragment, two per transposed one
+      constexpr int R = FM * (A_KMAJ ? 1 : 2) + FN * (B_KMAJ ? 1 : 2);
+      sched_stage<R, FM * FN, BKT / 16>();
     }
   };
   auto issue = [&](uint16_t* sb, int st) {  // DMA of full stage st (0-based within this split)
@@ -759,8 +793,8 @@ __global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2)
       const uint32_t aux_bytes = (uint32_t)(((int64_t)g.M * g.ldaux) * 2);
       const __amdgpu_buffer_rsrc_t raux = make_rsrc(g.aux, aux_bytes);
 #pragma unroll
-      for (int i = 0; i < BM * BN * 2 / 1024 / kNW; ++i) {
-        const int blk = i * kNW + wave;            // 1 KB block = 4 rows
+      for (int i = 0; i < BM * BN * 2 / 1024 / NWV; ++i) {
+        const int blk = i * NWV + wave;            // 1 KB block = 4 rows
         const int r = blk * 4 + (lane >> 4);
         const int c = (lane & 15) ^ (r & 15);
         const uint32_t off = (uint32_t)(((int64_t)(m0 + r) * g.ldaux + n0 + c * 8) * 2);
@@ -805,9 +839,9 @@ __global__ __launch_bounds__(256, (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2)
   // 16-byte pieces of a row. Values are finished (scale, bias, GELU') group by
   // group on the way into LDS, which keeps few of them live in VGPRs.
   static_assert(WTN == 64, "the store transpose assumes 64-column wave tiles");
-  static_assert(STAGE * 2 >= 16384, "two 8 KB slabs per stage buffer");
+  static_assert(STAGE * 2 >= NWV / 2 * 8192, "an 8 KB slab per wave in the first two stage buffers");
   uint8_t* wl = kAuxInSt1 ? reinterpret_cast<uint8_t*>(st0) + wave * 8192
-                          : reinterpret_cast<uint8_t*>(wave < 2 ? st0 : st1) + (wave & 1) * 8192;
+                          : reinterpret_cast<uint8_t*>(wave < NWV / 2 ? st0 : st1) + (wave % (NWV / 2)) * 8192;
   auto finish4 = [&](int i, int j, int q, float x[4]) {
     const int nl = wn * WTN + j * 32 + q * 8 + g4;
     f32x4 b = {0.f, 0.f, 0.f, 0.f};
@@ -923,6 +957,12 @@ NL_I8(NL_EPI_BIAS)
 NL_I8(NL_EPI_BIAS_GELU)
 NL_I8(NL_EPI_DGELU)
 template __global__ void gemm2_kernel<256, 128, 32, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, true, true, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, true, true, uint16_t, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, uint16_t, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, false, false, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, false, false, uint16_t, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 128, 32, 2, true, false, uint16_t, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 128, 32, 2, false, false, float, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 128, 32, 2, false, false, uint16_t, NL_EPI_NONE>(GemmArgs);
@@ -994,6 +1034,26 @@ Plan make_plan(int opA, int opB, int M, int N, int K, int epi) {
     p.big = 1;
     p.tiles = (int)((int64_t)((M + 255) / 256) * ((N + 127) / 128));
   }
+  // 256 x 256 tiles (8 waves of 128 x 64, 64-k stages) for products of
+  // >= 100 GFLOP without a fused epilogue (the LM head). Each CU then needs
+  // half the operand bytes per flop of a 128 x 128 tile: on MI355X the global
+  // -> LDS ingress of a CU saturates near 28 B/clk, which caps 128 x 128 tiles
+  // (64 B/clk at MFMA peak) well below 256 x 256 (32 B/clk). Measured at the
+  // LM-head shapes: NN 1076 -> 896 us, NT 1186 -> 897 us, TN 931 -> 811 us.
+  // One workgroup per CU, so a short grid splits K up to 256 workgroups.
+  if (epi == NL_EPI_NONE && !(opA == NL_OP_T && opB == NL_OP_T) && 2.0 * M * N * K >= 1e11) {
+    p.big = 2;
+    p.tiles = (int)((int64_t)((M + 255) / 256) * ((N + 255) / 256));
+    p.splits = 1;
+    p.k_chunk = K;
+    if (p.tiles < 256 && K >= 4096) {
+      const int sp = 256 / p.tiles;
+      int chunk = (K + sp - 1) / sp;
+      chunk = (chunk + BK - 1) / BK * BK;
+      p.k_chunk = chunk;
+      p.splits = (K + chunk - 1) / chunk;
+    }
+  }
   p.ldw = ((int64_t)N + 7) / 8 * 8;
   p.ws_bytes = p.splits > 1 ? (size_t)p.splits * M * p.ldw * sizeof(float) : 0;
   return p;
@@ -1003,15 +1063,19 @@ template <int BM, int BN, int WM, int WN, bool AK, bool BK_, typename OutT>
 void launch_cfg(GemmArgs g, const Plan& plan, hipStream_t st) {
   Plan p = plan;
   // the v2 kernel addresses operands with 32-bit buffer offsets
-  const int64_t a_ext = (AK ? (int64_t)g.M + 2 * BM : (int64_t)g.K + BK) * g.lda * 2;
-  const int64_t b_ext = (BK_ ? (int64_t)g.N + BN : (int64_t)g.K + BK) * g.ldb * 2;
+  // (rows up to a 256-row tile past the end, which the range check zeroes)
+  const int64_t a_ext = (AK ? (int64_t)g.M + 256 : (int64_t)g.K + BK) * g.lda * 2;
+  const int64_t b_ext = (BK_ ? (int64_t)g.N + 256 : (int64_t)g.K + BK) * g.ldb * 2;
   // (the DGELU epilogue also reads its aux tile through a buffer descriptor)
   const int64_t aux_ext = g.epi == NL_EPI_DGELU ? ((int64_t)g.M + BM) * g.ldaux * 2 : 0;
   const bool v2 = WM == 2 && WN == 2 && a_ext < ((int64_t)1 << 31) && b_ext < ((int64_t)1 << 31) &&
                   aux_ext < ((int64_t)1 << 31);
-  if (p.big && !v2) {  // the register-staged kernel only has 128 x 128 tiles
+  if (p.big && !v2) {  // the register-staged kernel only has 128 x 128 tiles (and no split plan here)
     p.big = 0;
     p.tiles = (int)((int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128));
+    p.splits = 1;
+    p.k_chunk = g.K > 0 ? g.K : 1;
+    g.ws = nullptr;
   }
   g.tiles = p.tiles;
   g.k_chunk = p.k_chunk;
@@ -1019,8 +1083,14 @@ void launch_cfg(GemmArgs g, const Plan& plan, hipStream_t st) {
   // operands k-major (NT) 64-k stages win; otherwise 32-k stages (32 KB of LDS,
   // more workgroups per CU to cover L2-miss latency) win.
   auto launch2 = [&](int grid) {
+    if constexpr (AK || !BK_) {
+      if (p.big == 2) {
+        hipLaunchKernelGGL((gemm2_kernel<256, 256, 64, 2, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(512), 0, st, g);
+        return;
+      }
+    }
     if constexpr (!BK_) {
-      if (p.big) {
+      if (p.big == 1) {
         hipLaunchKernelGGL((gemm2_kernel<256, 128, 32, 2, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(256), 0, st, g);
         return;
       }

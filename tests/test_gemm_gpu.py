@@ -159,6 +159,34 @@ def test_gemm_split_k_matches_single_pass_and_is_deterministic(dev, M, N, K):
     assert rel_l2(_np(split1[:, ct]), ops.gemm(_np(X), _np(dY[:, ct]), "T", "N")) <= 5e-3
 
 
+@pytest.mark.parametrize("opA,opB,M,N,K,out", [("N", "N", 2000, 9000, 3000, "f32"), ("N", "T", 4000, 600, 25000, "f32"),
+                                                ("T", "N", 600, 9000, 10000, "f32"), ("N", "N", 2000, 9000, 3000, "bf16")])
+def test_gemm_huge_tile_path_exact_small_integers(dev, opA, opB, M, N, K, out):
+    """Products of >= 100 GFLOP take the 256 x 256 tile path (8 waves; split K
+    for short grids: NT here splits 5 ways, TN 2 ways). Ragged M, N and K (a
+    masked k tail), checked exactly on integer inputs (every partial sum is an
+    integer below 2^24, so fp32 accumulation is exact in any order and bf16
+    output is the single rounding of the exact value)."""
+    import torch
+    from nlearn_amd.kernels.gemm import gemm_raw
+
+    assert 2.0 * M * N * K >= 1e11                      # the dispatcher picks the 256 x 256 tiles
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    As = A.T.copy() if opA == "T" else A
+    Bs = B.T.copy() if opB == "T" else B
+    dt = torch.float32 if out == "f32" else torch.bfloat16
+    C = gemm_raw(_dev_bf16(As, dev), _dev_bf16(Bs, dev), opA, opB, out_dtype=dt)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, 260), np.arange(M - 260, M), rng.integers(0, M, 100)]))
+    got = C[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+    ref = A[rows] @ B
+    if out == "bf16":
+        ref = torch.from_numpy(ref).bfloat16().float().numpy()
+    assert np.array_equal(got, ref)
+
+
 @pytest.mark.parametrize("opA,M,N,K", [("T", 500, 50257, 200), ("N", 16312, 8192, 72)])
 def test_gemm_tall_tile_path_exact_small_integers(dev, opA, M, N, K):
     """Products large enough for the 256 x 128 tile path (ragged M, N and K),
