@@ -441,7 +441,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 //   * K-major tile (rows x 64 k): [row][k] with the 16-byte-chunk XOR swizzle
 //     of the v1 kernel; MFMA fragments are single ds_read_b128.
 //   * MN-major tile (64 k x rows): stored as it sits in memory, [k][row], with
-//     chunk c of k-row k at slot c ^ (2k & 15); an MFMA fragment (8 k of one
+//     chunk c of k-row k at slot c ^ mnswz(k); an MFMA fragment (8 k of one
 //     row) is two ds_read_b64_tr_b16, which deliver 4 consecutive k of a column
 //     to each lane of a 16-lane group. No register transposes at all.
 //   * A ragged K tail (K % 64 != 0) is staged once through registers with
@@ -456,6 +456,13 @@ __device__ __forceinline__ int kswz(int r) {
   if constexpr (CH == 8) return (r ^ (r >> 3)) & 7;
   else return (r >> 1) & 3;
 }
+
+// Chunk swizzle of MN-major tiles. A transposing fragment read (32 lanes per
+// LDS cycle) touches chunks c0 + {0..3} of k-rows k0 + {0..3}; XOR with
+// 4 (k & 3) maps those 16 (chunk, k) pairs to 16 distinct slots mod 16, i.e.
+// all 64 banks (rows are 256 or 512 bytes). The former 2k swizzle paired them
+// up: 2-way conflicts, measured as 28% of LDS cycles on the LM-head NN GEMM.
+__device__ __forceinline__ int mnswz(int k) { return (4 * k) & 15; }
 
 // Per-lane DMA offsets of one ROWS x BKT operand tile filled by NW waves.
 template <int ROWS, int BKT, bool KMAJ, int NW>
@@ -474,7 +481,7 @@ struct Dma {
       } else {
         constexpr int CPR = ROWS / 8, RPI = 64 / CPR;
         const int k = (i * NW + wave) * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ ((2 * k) & 15);
+        const int c = (lane % CPR) ^ mnswz(k);
         voff[i] = (uint32_t)(((int64_t)k * ld + row0 + c * 8) * 2);
       }
     }
@@ -512,7 +519,7 @@ __device__ __forceinline__ void stage_masked(const uint16_t* __restrict__ P, int
       const int gk = k0 + k, gm = row0 + c * 8;
       u32x4 v = {0u, 0u, 0u, 0u};
       if (gk < k_lim) v = load8(P + (int64_t)gk * ld + gm, rows_lim - gm);
-      *reinterpret_cast<u32x4*>(lds + k * ROWS + ((c ^ ((2 * k) & 15)) << 3)) = v;
+      *reinterpret_cast<u32x4*>(lds + k * ROWS + ((c ^ mnswz(k)) << 3)) = v;
     }
   }
 }
@@ -535,7 +542,7 @@ struct Frag {
 #pragma unroll
       for (int rr = 0; rr < 2; ++rr) {
         const int k = 8 * g + 4 * rr + (j >> 2);  // + ks*16 (does not change the swizzle key)
-        off[rr] = k * ROWS + (((mn >> 3) ^ ((2 * k) & 15)) << 3) + (mn & 7);
+        off[rr] = k * ROWS + (((mn >> 3) ^ mnswz(k)) << 3) + (mn & 7);
       }
       sw = 0;
     }
