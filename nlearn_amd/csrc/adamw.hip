@@ -85,22 +85,27 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
   if (e0 >= e1) return;  // only with a launch larger than the prepared chunk count
   // leaves are 16-byte aligned and chunks start at multiples of 4: vec4 body, scalar tail
   const int64_t v1 = e0 + ((e1 - e0) & ~(int64_t)3);
-  for (int64_t e = e0 + threadIdx.x * 4; e < v1; e += 256 * 4) {
-    const f32x4 gi = *reinterpret_cast<const f32x4*>(t.g + e);
-    f32x4 m = *reinterpret_cast<const f32x4*>(t.m + e);
-    f32x4 v = *reinterpret_cast<const f32x4*>(t.v + e);
-    f32x4 p = *reinterpret_cast<const f32x4*>(t.p + e);
+  // p, g, m and v stream through once per step (nontemporal); the bf16 shadow
+  // is read again by the next forward pass and stays cacheable. The lane's
+  // (row, column) advances incrementally instead of by a 64-bit division.
+  int64_t e = e0 + threadIdx.x * 4;
+  int64_t r = t.shadow && t.cols > 0 ? e / t.cols : 0;
+  int64_t c = e - r * t.cols;
+  for (; e < v1; e += 256 * 4) {
+    const f32x4 gi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.g + e));
+    f32x4 m = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.m + e));
+    f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.v + e));
+    f32x4 p = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.p + e));
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       float mk = m[k], vk = v[k], pk = p[k];
       adam1(gi[k], mk, vk, pk, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
       m[k] = mk, v[k] = vk, p[k] = pk;
     }
-    *reinterpret_cast<f32x4*>(t.m + e) = m;
-    *reinterpret_cast<f32x4*>(t.v + e) = v;
-    *reinterpret_cast<f32x4*>(t.p + e) = p;
+    __builtin_nontemporal_store(m, reinterpret_cast<f32x4*>(t.m + e));
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(t.v + e));
+    __builtin_nontemporal_store(p, reinterpret_cast<f32x4*>(t.p + e));
     if (t.shadow) {
-      const int64_t r = e / t.cols, c = e - r * t.cols;
       const int64_t o = r * t.ld_shadow + c;
       if (c + 4 <= t.cols && (o & 3) == 0) {
         *reinterpret_cast<u32x2*>(t.shadow + o) = u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
@@ -111,9 +116,14 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
           t.shadow[rk * t.ld_shadow + ck] = f32_to_bf16(p[k]);
         }
       }
+      c += 256 * 4;
+      while (c >= t.cols) {
+        c -= t.cols;
+        ++r;
+      }
     }
   }
-  for (int64_t e = v1 + threadIdx.x; e < e1; e += 256) {
+  for (e = v1 + threadIdx.x; e < e1; e += 256) {
     float m = t.m[e], v = t.v[e], p = t.p[e];
     adam1(t.g[e], m, v, p, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
     t.m[e] = m;

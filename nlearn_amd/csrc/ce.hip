@@ -10,7 +10,8 @@
 // sees exactly one read and one write of the row: per-lane (max, sum) ->
 // wavefront butterfly -> 8-wave LDS combine -> lse -> dlogits straight from
 // registers, optionally written over the logits in place. Rows whose start is
-// not 16-byte aligned (dense V = 50257) peel <8 head and tail elements.
+// not 16-byte aligned (dense V = 50257) peel <8 head and tail elements. The
+// row is streamed with nontemporal loads and stores (read once, written once).
 #include "common.h"
 
 namespace nl {
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_rowreg_kernel(
 #pragma unroll
   for (int j = 0; j < NVEC; ++j) {
     const int idx = j * kCeBlock + tid;
-    if (idx < rs.nbody) v[j] = body[idx];
+    if (idx < rs.nbody) v[j] = __builtin_nontemporal_load(body + idx);
   }
   // one optional scalar element: head (tid < head) or tail (8 <= tid < 8 + tail)
   int eidx = -1;
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(kCeBlock) void ce_rowreg_kernel(
         u32x4 o;
 #pragma unroll
         for (int q = 0; q < 4; ++q) o[q] = pack_bf16x2(p[2 * q], p[2 * q + 1]);
-        dbody[j * kCeBlock + tid] = o;
+        __builtin_nontemporal_store(o, dbody + j * kCeBlock + tid);
       }
     }
     if (eidx >= 0) {
