@@ -190,8 +190,27 @@ struct OutOp {
   }
 };
 
+// Workgroup id -> (tile rank, head, batch) over a 1-D grid with the rank
+// slowest. The hardware deals consecutive workgroups to the 8 XCDs in turn, so
+// every rank (causal work per tile grows with it, up to ntiles x) spreads
+// evenly over the XCDs and their CUs. With the tile index fastest and a
+// power-of-two tile count, all the heaviest tiles would land on the same XCDs.
+struct TileCoord {
+  int rank, h, b;
+};
+__device__ __forceinline__ TileCoord tile_coord(int H, int B) {
+  const int bh = H * B;
+  const int id = (int)blockIdx.x;
+  TileCoord t;
+  t.rank = id / bh;
+  const int r = id - t.rank * bh;
+  t.b = r / H;
+  t.h = r - t.b * H;
+  return t;
+}
+
 struct FwdArgs {
-  int S, causal;
+  int S, causal, H, B;
   float scale_log2;
   Op q, k, v;
   OutOp o;
@@ -224,8 +243,9 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sV1[kBlk * kD];
   const int S = a.S;
   const int nqt = (S + kRows - 1) / kRows;
-  const int qt = nqt - 1 - (int)blockIdx.x;  // heaviest (latest) query tiles first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const TileCoord tc = tile_coord(a.H, a.B);
+  const int qt = nqt - 1 - tc.rank;  // heaviest (latest) query tiles first
+  const int h = tc.h, b = tc.b;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int qw0 = qt * kRows + wave * 32;  // first query of this wave
@@ -328,7 +348,7 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
   if (qvalid) {
     const float inv = 1.f / lt;
     store_row64(a.o.at(b, h, q), o, inv, g);
-    if (g == 0) a.L[((int64_t)b * gridDim.y + h) * S + q] = (m + fast_log2(lt)) * kLn2;
+    if (g == 0) a.L[((int64_t)b * a.H + h) * S + q] = (m + fast_log2(lt)) * kLn2;
   }
 }
 
@@ -362,7 +382,7 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(PreArgs a) {
 }
 
 struct BwdArgs {
-  int S, causal;
+  int S, causal, H, B;
   float scale, scale_log2;
   Op q, k, v, dout;
   const float* L;  // natural-log lse
@@ -386,14 +406,15 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
   __shared__ __attribute__((aligned(16))) float sD0[kBlk];
   __shared__ __attribute__((aligned(16))) float sD1[kBlk];
   const int S = a.S;
-  const int kt_idx = blockIdx.x;  // low key tiles see the most queries: launched first
-  const int h = blockIdx.y, b = blockIdx.z;
+  const TileCoord tc = tile_coord(a.H, a.B);
+  const int kt_idx = tc.rank;  // low key tiles see the most queries: launched first
+  const int h = tc.h, b = tc.b;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int kw0 = kt_idx * kRows + wave * 32;
   const int key = kw0 + l32;
   const bool kvalid = key < S;
-  const int64_t lbase = ((int64_t)b * gridDim.y + h) * S;
+  const int64_t lbase = ((int64_t)b * a.H + h) * S;
 
   bf16x8 kf[4], vf[4];
   {
@@ -503,14 +524,15 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sV1[kBlk * kD];
   const int S = a.S;
   const int nqt = (S + kRows - 1) / kRows;
-  const int qt = nqt - 1 - (int)blockIdx.x;
-  const int h = blockIdx.y, b = blockIdx.z;
+  const TileCoord tc = tile_coord(a.H, a.B);
+  const int qt = nqt - 1 - tc.rank;
+  const int h = tc.h, b = tc.b;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
   const int qw0 = qt * kRows + wave * 32;
   const int q = qw0 + l32;
   const bool qvalid = q < S;
-  const int64_t lbase = ((int64_t)b * gridDim.y + h) * S;
+  const int64_t lbase = ((int64_t)b * a.H + h) * S;
 
   bf16x8 qf[4], df[4];
   {
@@ -642,8 +664,11 @@ extern "C" int nl_flash_attention_fwd(void* stream, int batch, int heads, int se
   a.v = Op{V, sv};
   a.o = OutOp{O, so};
   a.L = L;
-  dim3 grid((seq + kRows - 1) / kRows, heads, batch);
-  hipLaunchKernelGGL(flash_fwd_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+  a.H = heads;
+  a.B = batch;
+  const int64_t wgs = (int64_t)((seq + kRows - 1) / kRows) * heads * batch;
+  if (wgs >= ((int64_t)1 << 31)) return nl_set_error(NL_EUNSUPPORTED, "flash: too many tiles");
+  hipLaunchKernelGGL(flash_fwd_kernel, dim3((unsigned)wgs), dim3(kThreads), 0, (hipStream_t)stream, a);
   return nl_check_launch("nl_flash_attention_fwd");
 }
 
@@ -691,6 +716,15 @@ static int fill_bwd(BwdArgs& a, int seq, int causal, float scale, const nl_bf16*
   return NL_OK;
 }
 
+static int bwd_grid(int batch, int heads, int seq, BwdArgs& a, dim3& grid) {
+  a.H = heads;
+  a.B = batch;
+  const int64_t wgs = (int64_t)((seq + kRows - 1) / kRows) * heads * batch;
+  if (wgs >= ((int64_t)1 << 31)) return nl_set_error(NL_EUNSUPPORTED, "flash: too many tiles");
+  grid = dim3((unsigned)wgs);
+  return NL_OK;
+}
+
 extern "C" int nl_flash_attention_bwd_dq(void* stream, int batch, int heads, int seq, int d_head, float scale,
                                          int causal, const nl_bf16* Q, nl_attn_stride sq, const nl_bf16* K,
                                          nl_attn_stride sk, const nl_bf16* V, nl_attn_stride sv,
@@ -702,7 +736,8 @@ extern "C" int nl_flash_attention_bwd_dq(void* stream, int batch, int heads, int
   NL_TRY(fill_bwd(a, seq, causal, scale, Q, sq, K, sk, V, sv, dO, sdo, L, D));
   NL_TRY(check_op(dQ, sdq, "dQ"));
   a.dq = OutOp{dQ, sdq};
-  dim3 grid((seq + kRows - 1) / kRows, heads, batch);
+  dim3 grid;
+  NL_TRY(bwd_grid(batch, heads, seq, a, grid));
   hipLaunchKernelGGL(flash_bwd_dq_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
   return nl_check_launch("nl_flash_attention_bwd_dq");
 }
@@ -720,7 +755,8 @@ extern "C" int nl_flash_attention_bwd_dkdv(void* stream, int batch, int heads, i
   NL_TRY(check_op(dV, sdv, "dV"));
   a.dk = OutOp{dK, sdk};
   a.dv = OutOp{dV, sdv};
-  dim3 grid((seq + kRows - 1) / kRows, heads, batch);
+  dim3 grid;
+  NL_TRY(bwd_grid(batch, heads, seq, a, grid));
   hipLaunchKernelGGL(flash_bwd_dkdv_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
   return nl_check_launch("nl_flash_attention_bwd_dkdv");
 }
