@@ -28,6 +28,8 @@
 //     loads are in flight while the current one is consumed.
 //   * Causal work skipping per wave; fully masked waves only join the barriers.
 //     The heaviest tiles are launched first.
+#include <type_traits>
+
 #include "common.h"
 
 namespace nl {
@@ -286,20 +288,26 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) s[kt] = mfma32(frag_R<kAlongRows>(sk, kt * 32 + l32, ks * 2 + g), qf[ks], s[kt]);
     }
+    // One uniform branch per block between a masked and an unmasked variant
+    // (a per-element test of a uniform flag compiles to one branch per score).
     const bool need_mask = (a.causal && k0 + kBlk - 1 > qw0) || (k0 + kBlk > S);
     float bm = -INFINITY;
+    auto mask_max = [&](auto masked) {
+      const int lim = a.causal ? min(q, S - 1) : S - 1;  // last visible key
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[kt][r];
-        if (need_mask) {
-          const int key = k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (key >= S || (a.causal && key > q)) x = -INFINITY;
+        for (int r = 0; r < 16; ++r) {
+          float x = s[kt][r];
+          if constexpr (decltype(masked)::value) {
+            if (k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) > lim) x = -INFINITY;
+          }
+          s[kt][r] = x;
+          bm = fmaxf(bm, x);
         }
-        s[kt][r] = x;
-        bm = fmaxf(bm, x);
-      }
+    };
+    if (need_mask) mask_max(std::true_type{});
+    else mask_max(std::false_type{});
     bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
     const float mn = fmaxf(m, bm * c);
     const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
@@ -465,23 +473,28 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
         dp = mfma32(frag_R(so, qt * 32 + l32, ks * 2 + g), vf[ks], dp);
       }
       // lane (key, g) holds query rows qt*32 + 8qq + 4g + t
+      auto probs = [&](auto masked) {
+        const int lo = a.causal ? key : 0;  // first query that sees this key
 #pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int qr = qt * 32 + qq * 8 + 4 * g;
-        const f32x4 L4 = *reinterpret_cast<const f32x4*>(sl + qr);
-        const f32x4 D4 = *reinterpret_cast<const f32x4*>(sd + qr);
+        for (int qq = 0; qq < 4; ++qq) {
+          const int qr = qt * 32 + qq * 8 + 4 * g;
+          const f32x4 L4 = *reinterpret_cast<const f32x4*>(sl + qr);
+          const f32x4 D4 = *reinterpret_cast<const f32x4*>(sd + qr);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const int r = 4 * qq + t;
-          float p = fast_exp2(__builtin_fmaf(s[r], c, -L4[t] * kLog2e));
-          if (need_mask) {
-            const int qi = q0 + qr + t;
-            if (qi >= S || (a.causal && qi < key)) p = 0.f;
+          for (int t = 0; t < 4; ++t) {
+            const int r = 4 * qq + t;
+            float p = fast_exp2(__builtin_fmaf(s[r], c, -L4[t] * kLog2e));
+            if constexpr (decltype(masked)::value) {
+              const int qi = q0 + qr + t;
+              if (qi >= S || qi < lo) p = 0.f;
+            }
+            s[r] = p;
+            dp[r] = p * (dp[r] - D4[t]);
           }
-          s[r] = p;
-          dp[r] = p * (dp[r] - D4[t]);
         }
-      }
+      };
+      if (need_mask) probs(std::true_type{});
+      else probs(std::false_type{});
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const bf16x8 pf = pack_frag(s, hh);
@@ -576,15 +589,19 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(BwdArgs a) {
         s = mfma32(frag_R(sk, kt * 32 + l32, ks * 2 + g), qf[ks], s);
         dp = mfma32(frag_R(sv, kt * 32 + l32, ks * 2 + g), df[ks], dp);
       }
+      auto probs = [&](auto masked) {
+        const int lim = a.causal ? min(q, S - 1) : S - 1;  // last visible key
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(__builtin_fmaf(s[r], c, nLq));
-        if (need_mask) {
-          const int kk = k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (kk >= S || (a.causal && kk > q)) p = 0.f;
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(__builtin_fmaf(s[r], c, nLq));
+          if constexpr (decltype(masked)::value) {
+            if (k0 + kt * 32 + 8 * (r >> 2) + 4 * g + (r & 3) > lim) p = 0.f;
+          }
+          dp[r] = p * (dp[r] - Dq);
         }
-        dp[r] = p * (dp[r] - Dq);
-      }
+      };
+      if (need_mask) probs(std::true_type{});
+      else probs(std::false_type{});
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const bf16x8 dsf = pack_frag(dp, hh);
