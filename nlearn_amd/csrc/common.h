@@ -37,8 +37,12 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   __bf16 b = (__bf16)f;
   return __builtin_bit_cast(uint16_t, b);
 }
+// Two floats -> one dword of bf16 (lo in bits 0-15): a single v_cvt_pk_bf16_f32
+// (converting each half separately costs two conversions and a v_or).
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2_cvt;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_cvt;
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_cvt){lo, hi}, bf16x2_cvt));
 }
 
 // ---------------------------------------------------------------------------

@@ -323,10 +323,14 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
       }
     l = __builtin_fmaf(l, alpha, rs);
     m = mn;
+    // alpha == 1 exactly when the running max did not move; once the max has
+    // settled, whole blocks leave every row's max in place and skip the rescale
+    if (__ballot(alpha != 1.f)) {
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt)
+      for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+        for (int r = 0; r < 16; ++r) o[dt][r] *= alpha;
+    }
     // O^T (d x queries) += V^T P^T, P straight from the registers
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
