@@ -468,9 +468,15 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
     const bool need_mask = (a.causal && q0 < kw0 + 31) || (q0 + kBlk > S);
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
+      // dP - D straight from the product: its accumulator starts at -D
       f32x16 s, dp;
       zero(s);
-      zero(dp);
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const f32x4 nD4 = *reinterpret_cast<const f32x4*>(sd + qt * 32 + qq * 8 + 4 * g);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) dp[4 * qq + t] = nD4[t];
+      }
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         s = mfma32(frag_R(sq, qt * 32 + l32, ks * 2 + g), kf[ks], s);
@@ -482,18 +488,17 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
 #pragma unroll
         for (int qq = 0; qq < 4; ++qq) {
           const int qr = qt * 32 + qq * 8 + 4 * g;
-          const f32x4 L4 = *reinterpret_cast<const f32x4*>(sl + qr);
-          const f32x4 D4 = *reinterpret_cast<const f32x4*>(sd + qr);
+          const f32x4 nL4 = *reinterpret_cast<const f32x4*>(sl + qr);  // -L log2(e)
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
             const int r = 4 * qq + t;
-            float p = fast_exp2(__builtin_fmaf(s[r], c, -L4[t] * kLog2e));
+            float p = fast_exp2(__builtin_fmaf(s[r], c, nL4[t]));
             if constexpr (decltype(masked)::value) {
               const int qi = q0 + qr + t;
               if (qi >= S || qi < lo) p = 0.f;
             }
             s[r] = p;
-            dp[r] = p * (dp[r] - D4[t]);
+            dp[r] = p * dp[r];
           }
         }
       };
@@ -512,14 +517,29 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
     }
   };
 
+  // Once a block's L and D have landed, the lanes that fetched them rewrite
+  // them in place as -L log2(e) and -D (one vector op each per block instead of
+  // one per score in every wave).
+  auto prep = [&](float* sl, float* sd) {
+    if (lane < 16 && wave < 2) {
+      float* p = (wave == 0 ? sl : sd) + lane * 4;
+      const float f = wave == 0 ? -kLog2e : -1.f;
+      f32x4 x = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] *= f;
+      *reinterpret_cast<f32x4*>(p) = x;
+    }
+  };
   if (nqb > 0) issue(sQ0, sO0, sL0, sD0, 0);
   for (int qb = 0; qb < nqb; qb += 2) {
     wait_vm<0>();
+    prep(sL0, sD0);
     __syncthreads();
     if (qb + 1 < nqb) issue(sQ1, sO1, sL1, sD1, qb + 1);
     compute(sQ0, sO0, sL0, sD0, qb);
     if (qb + 1 >= nqb) break;
     wait_vm<0>();
+    prep(sL1, sD1);
     __syncthreads();
     if (qb + 2 < nqb) issue(sQ0, sO0, sL0, sD0, qb + 2);
     compute(sQ1, sO1, sL1, sD1, qb + 1);
