@@ -18,8 +18,9 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
+from . import wgrad
 from .gemm import (EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU, _check_device, _kernel_ready, _ld, bf16_shadow, gemm_raw,
-                   grad_buffer, padded_empty)
+                   grad_buffer, padded_empty, weight_grad)
 
 _BF16 = torch.bfloat16
 _F32 = torch.float32
@@ -125,6 +126,13 @@ class _AddLayerNorm(torch.autograd.Function):
         return dx, dx, *_unless_buffered(ctx.bufs, (dg, db)), None
 
 
+def _wgrad(X, dY, buf):
+    """X^T . dY into the gradient buffer (forked when overlapping), or a fresh fp32 tensor."""
+    if buf is not None:
+        return weight_grad(X, dY, buf)
+    return gemm_raw(X, dY, "T", "N", out_dtype=_F32)
+
+
 def _unless_buffered(bufs, grads):
     """Gradients to hand back to autograd: None where a main_grad buffer took them."""
     return tuple(None if b is not None else g for b, g in zip(bufs, grads))
@@ -147,16 +155,24 @@ def add_layer_norm(x: torch.Tensor, r: torch.Tensor, gamma: torch.Tensor, beta: 
 
 
 def colsum(x2: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
-    """fp32 column sums of a bf16 [rows, cols] matrix (fixed summation order)."""
+    """fp32 column sums of a bf16 [rows, cols] matrix (fixed summation order).
+
+    With a preallocated ``out`` (a bias gradient buffer) the kernels are forked
+    onto the weight-gradient stream when one is active (kernels.wgrad)."""
     rows, cols = x2.shape
     x2 = _kernel_ready(x2)
-    if out is None:
+    fresh = out is None
+    if fresh:
         out = torch.empty(cols, dtype=_F32, device=x2.device)
     wsb = int(_lib.load().nl_colsum_ws_bytes(rows, cols))
     ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=x2.device)
-    _lib.call("nl_colsum_bf16", _stream(x2), rows, cols, x2.data_ptr(), _ld(x2), out.data_ptr(), 0, ws.data_ptr(),
-              wsb)
-    return out
+
+    def run():
+        _lib.call("nl_colsum_bf16", _stream(x2), rows, cols, x2.data_ptr(), _ld(x2), out.data_ptr(), 0,
+                  ws.data_ptr(), wsb)
+        return out
+
+    return run() if fresh else wgrad.fork(run, x2, out, ws)
 
 
 # ---------------------------------------------------------------------------
@@ -189,11 +205,11 @@ class _FFN(torch.autograd.Function):
         gW1, gb1, gW2, gb2 = ctx.bufs
         dy2 = _rows(dy)
         db2 = colsum(dy2, out=gb2)
-        dW2 = gemm_raw(h, dy2, "T", "N", out_dtype=_F32, out=gW2)                 # h^T . dy
+        dW2 = _wgrad(h, dy2, gW2)                                                  # h^T . dy
         du = padded_empty(u.shape[0], u.shape[1], _BF16, dy2.device)
         gemm_raw(dy2, W2b, "N", "T", out=du, epi=EPI_DGELU, aux=u)               # (dy . W2^T) * gelu'(u)
         db1 = colsum(du, out=gb1)
-        dW1 = gemm_raw(x2, du, "T", "N", out_dtype=_F32, out=gW1)                 # x^T . du
+        dW1 = _wgrad(x2, du, gW1)                                                  # x^T . du
         dx = gemm_raw(du, W1b, "N", "T", out_dtype=_BF16)                          # du . W1^T
         return dx.view(ctx.shape), *_unless_buffered(ctx.bufs, (dW1, db1, dW2, db2))
 

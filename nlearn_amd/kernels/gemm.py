@@ -23,6 +23,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
+from . import wgrad
 
 _BF16 = torch.bfloat16
 _F32 = torch.float32
@@ -78,12 +79,13 @@ EPI_NONE, EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU = 0, 1, 2, 3
 def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", out_dtype=_F32,
              out: torch.Tensor | None = None, alpha: float = 1.0, beta: float = 0.0,
              alpha_dev: torch.Tensor | None = None, epi: int = EPI_NONE, bias: torch.Tensor | None = None,
-             aux: torch.Tensor | None = None) -> torch.Tensor:
+             aux: torch.Tensor | None = None, ws: torch.Tensor | None = None) -> torch.Tensor:
     """C = epilogue(alpha * [*alpha_dev] * op(A) @ op(B)) on the current stream.
 
     opA == "T": A is stored [K, M]; opB == "T": B is stored [N, K].
     epi: EPI_NONE (+ beta * C), EPI_BIAS (+ bias[N] + beta * C), EPI_BIAS_GELU
     (aux = bf16(v + bias), C = gelu_tanh(aux)), EPI_DGELU (C = v * gelu_tanh'(aux)).
+    ws: split-K workspace of at least ``gemm_ws_bytes`` bytes (allocated here if None).
     """
     _check_device(A, B)
     A = _kernel_ready(A)
@@ -114,7 +116,10 @@ def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", o
     oa = _lib.NL_OP_T if opA == "T" else _lib.NL_OP_N
     ob = _lib.NL_OP_T if opB == "T" else _lib.NL_OP_N
     wsb = int(_lib.load().nl_gemm_ws_bytes(oa, ob, M, N, K))
-    ws = torch.empty(wsb // 4, dtype=_F32, device=A.device) if wsb else None
+    if ws is None:
+        ws = torch.empty(wsb // 4, dtype=_F32, device=A.device) if wsb else None
+    elif ws.numel() * ws.element_size() < wsb:
+        raise ValueError("gemm: workspace too small")
     _lib.call("nl_gemm_fused", stream, oa, ob, M, N, K, float(alpha),
               A.data_ptr(), _ld(A), B.data_ptr(), _ld(B), float(beta), out.data_ptr(),
               _lib.NL_DTYPE_F32 if out.dtype == _F32 else _lib.NL_DTYPE_BF16, _ld(out),
@@ -122,6 +127,25 @@ def gemm_raw(A: torch.Tensor, B: torch.Tensor, opA: str = "N", opB: str = "N", o
               bias.data_ptr() if bias is not None else None,
               aux.data_ptr() if aux is not None else None, _ld(aux) if aux is not None else 0,
               ws.data_ptr() if ws is not None else None, wsb)
+    return out
+
+
+def gemm_ws(opA: str, opB: str, M: int, N: int, K: int, device) -> torch.Tensor | None:
+    """The split-K workspace gemm_raw would allocate for this product (or None)."""
+    oa = _lib.NL_OP_T if opA == "T" else _lib.NL_OP_N
+    ob = _lib.NL_OP_T if opB == "T" else _lib.NL_OP_N
+    wsb = int(_lib.load().nl_gemm_ws_bytes(oa, ob, M, N, K))
+    return torch.empty(wsb // 4, dtype=_F32, device=device) if wsb else None
+
+
+def weight_grad(X: torch.Tensor, dY: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """out = X^T . dY (fp32), forked onto the weight-gradient stream when one is
+    active (nlearn_amd.kernels.wgrad); operands and workspace are prepared on
+    the current stream first, so the forked kernels allocate nothing."""
+    X = _kernel_ready(X)
+    dY = _kernel_ready(dY)
+    ws = gemm_ws("T", "N", X.shape[1], dY.shape[1], X.shape[0], X.device)
+    wgrad.fork(lambda: gemm_raw(X, dY, "T", "N", out=out, ws=ws), X, dY, out, ws)
     return out
 
 
@@ -221,7 +245,7 @@ class _Linear(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             mg = grad_buffer(W)
             if mg is not None:
-                gemm_raw(x2, dy, "T", "N", out=mg)                                 # X^T . dY -> main_grad
+                weight_grad(x2, dy, mg)                                            # X^T . dY -> main_grad
             else:
                 dW = gemm_raw(x2, dy, "T", "N", out_dtype=_F32 if W.dtype == _F32 else W.dtype)
         return dx, dW

@@ -15,6 +15,7 @@ tokenizer, no wandb (the reference needs all three, train.py:433-443,515-535).
 from __future__ import annotations
 
 import argparse
+import contextlib
 import math
 import os
 import time
@@ -22,6 +23,7 @@ import time
 import torch
 
 from . import _lib
+from .kernels import wgrad
 from .kernels.cross_entropy import cross_entropy
 from .model import BASELINE, ModelConfig, count_params, init_model, model_forward, tree_leaves
 
@@ -179,6 +181,7 @@ class AdamW:
 
     def apply(self, params, state: dict) -> None:
         """Launch the update with the scalars already on the device (no host sync)."""
+        wgrad.join()  # gradients forked onto the weight-gradient stream must be complete
         leaves = tree_leaves(params)
         stream = torch.cuda.current_stream(leaves[0].device).cuda_stream
         if all(getattr(p, "main_grad", None) is not None for p in leaves):
@@ -212,7 +215,8 @@ class AdamW:
         return state
 
 
-def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool = False, warmup: int = 2):
+def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool = False, warmup: int = 2,
+                    overlap_wgrad: bool = True):
     """train_step(params, opt_state, batch) -> (params, opt_state, loss).
 
     Parameters are updated in place; the loss is a 0-d device tensor (no host
@@ -222,25 +226,38 @@ def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool =
     AdamW) is captured once into a HIP graph and replayed; the batch is copied
     into the graph's input buffer and lr / bias corrections are written to the
     device before each replay.
+
+    overlap_wgrad: run the weight-gradient kernels on a second stream beside
+    the input-gradient chain (kernels.wgrad); results are identical.
     """
+    overlap = wgrad.overlap_weight_grads if overlap_wgrad else _no_overlap
 
     def eager_step(params, opt_state, batch):
         for p in tree_leaves(params):
             p.grad = None
         loss = batch_loss(params, batch, cfg)
-        loss.backward()
+        # weight gradients run on a second stream beside the dX chain; the
+        # context joins it before the optimizer reads the gradient buffers
+        with overlap(loss.device):
+            loss.backward()
         with torch.no_grad():
             opt_state = optimizer.update(params, opt_state)
         return params, opt_state, loss.detach()
 
     if not graph:
         return eager_step
-    return _GraphedStep(optimizer, cfg, eager_step, warmup)
+    return _GraphedStep(optimizer, cfg, eager_step, warmup, overlap)
+
+
+@contextlib.contextmanager
+def _no_overlap(device=None):
+    yield
 
 
 class _GraphedStep:
-    def __init__(self, optimizer, cfg, eager_step, warmup):
+    def __init__(self, optimizer, cfg, eager_step, warmup, overlap):
         self.opt, self.cfg, self.eager_step, self.warmup = optimizer, cfg, eager_step, warmup
+        self.overlap = overlap
         self.done = 0
         self.graph = None
         self.static_batch = None
@@ -253,11 +270,13 @@ class _GraphedStep:
         self.static_batch = batch.detach().clone()
         for p in leaves:
             p.grad = None
+        wgrad.prepare(batch.device)  # create the side stream outside the capture
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             loss = batch_loss(params, self.static_batch, self.cfg)
-            loss.backward()
+            with self.overlap(loss.device):
+                loss.backward()
             with torch.no_grad():
                 self.opt.apply(params, state)
         self.static_loss = loss.detach()
