@@ -38,6 +38,9 @@ def _args():
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the LM-head GEMM and a 1 GiB copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write profiles/traffic.json from the rocprofv3 CSV output of the two --pmc runs "
+                         "(FETCH_SIZE, WRITE_SIZE) over --traffic-probe")
     return ap.parse_args()
 
 
@@ -174,6 +177,72 @@ def traffic_probe(reps: int = 5) -> None:
     print(json.dumps({"probe": "traffic", "shape": [M, N, K], "copy_bytes": 2**30, "reps": reps}))
 
 
+def _probe_kernel_tag(name: str):
+    """bench.py tag of a kernel dispatched by --traffic-probe (None for others).
+    GEMM layouts are told apart by the A/B k-major template arguments."""
+    if "copyBuffer" in name:
+        return "copy"
+    if "splitk_reduce_kernel" in name:
+        return "gemm_NT_16384x512x50257"      # the only split product of the probe
+    if "gemm" in name and "<" in name:
+        args = [t.strip() for t in name.split("<", 1)[1].split(",")]
+        if len(args) >= 6:
+            layout = (args[4], args[5])
+            return {("true", "false"): "gemm_NN_16384x50257x512", ("true", "true"): "gemm_NT_16384x512x50257",
+                    ("false", "false"): "gemm_TN_512x50257x16384"}.get(layout)
+    return None
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> None:
+    """HBM bytes per launch of the probe's GEMMs from two rocprofv3 --pmc runs:
+    each counter's median over the probe's repetitions, summed over the kernels
+    of one product (the split NT adds its reduction), scaled by what the same
+    counter reads for the 1 GiB copy (known bytes)."""
+    import csv
+    import glob
+    import statistics
+
+    def read(d, counter):
+        per = {}          # tag -> kernel name -> [KiB per dispatch]
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                tag = _probe_kernel_tag(r["Kernel_Name"])
+                if tag:
+                    per.setdefault(tag, {}).setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        return {t: {k: statistics.median(v) for k, v in ks.items()} for t, ks in per.items()}
+
+    fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
+    copy_bytes = 2 ** 30
+    cf = sum(fetch["copy"].values())
+    cw = sum(write["copy"].values())
+    fs, ws = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
+    M, N, K = 16384, 50257, 512
+    algo = {"gemm_NN_16384x50257x512": 2 * (M * K + K * N + M * N),
+            "gemm_NT_16384x512x50257": 2 * (M * N + K * N + M * K),
+            "gemm_TN_512x50257x16384": 2 * (M * K + M * N) + 4 * K * N}
+    out = {"calibration": {"kernel": "__amd_rocclr_copyBuffer (torch copy_ of 1 GiB fp32)", "bytes": copy_bytes,
+                           "fetch_kib_raw": cf, "write_kib_raw": cw, "fetch_scale": round(fs, 4),
+                           "write_scale": round(ws, 4)},
+           "commands": ["rocprofv3 --pmc FETCH_SIZE --kernel-trace --output-format csv -d <fetch> -o run -- "
+                        "python3 <repo>/bench.py --traffic-probe",
+                        "rocprofv3 --pmc WRITE_SIZE --kernel-trace --output-format csv -d <write> -o run -- "
+                        "python3 <repo>/bench.py --traffic-probe",
+                        "python3 bench.py --traffic-summary <fetch> <write>"],
+           "kernels": {}}
+    for tag, a in algo.items():
+        fk, wk = sum(fetch.get(tag, {}).values()), sum(write.get(tag, {}).values())
+        fb, wb = int(fk * 1024 * fs), int(wk * 1024 * ws)
+        out["kernels"][tag] = {"dispatch_kernels": sorted(fetch.get(tag, {})), "fetch_kib_raw": fk,
+                               "write_kib_raw": wk, "fetch_bytes": fb, "write_bytes": wb,
+                               "bytes_per_launch": fb + wb, "algorithmic_bytes": a,
+                               "traffic_over_algorithmic": round((fb + wb) / a, 3)}
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps({k: v["bytes_per_launch"] for k, v in out["kernels"].items()}))
+
+
 def load_traffic(tag: str):
     """HBM bytes per launch of `tag` from the committed PMC summary, if it covers it."""
     try:
@@ -189,6 +258,9 @@ def main():
     a = _args()
     if a.traffic_probe:
         traffic_probe()
+        return
+    if a.traffic_summary:
+        traffic_summary(*a.traffic_summary)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the data-parallel step would all-reduce "
