@@ -30,6 +30,7 @@ import math
 import torch
 
 from . import _lib
+from .kernels import wgrad
 from .kernels.gemm import _check_device
 
 _BF16 = torch.bfloat16
@@ -89,11 +90,27 @@ def flash_bwd_raw4(q, k, v, O, dO, L, causal=True, scale=None, dq=None, dk=None,
     dk = _new_bshd(B, H, S, D, q.device) if dk is None else dk
     dv = _new_bshd(B, H, S, D, q.device) if dv is None else dv
     ws = torch.empty(max(_lib.ws_bytes(B, H, S), 16) // 4, dtype=torch.float32, device=q.device)
-    _lib.call("nl_flash_attention_bwd", _stream(q), B, H, S, D, scale, int(bool(causal)),
-              q.data_ptr(), _stride4(q), k.data_ptr(), _stride4(k), v.data_ptr(), _stride4(v),
-              O.data_ptr(), _stride4(O), dO.data_ptr(), _stride4(dO), L.contiguous().data_ptr(),
-              dq.data_ptr(), _stride4(dq), dk.data_ptr(), _stride4(dk), dv.data_ptr(), _stride4(dv),
-              ws.data_ptr())
+    L = L.contiguous()
+    if not wgrad.active():
+        _lib.call("nl_flash_attention_bwd", _stream(q), B, H, S, D, scale, int(bool(causal)),
+                  q.data_ptr(), _stride4(q), k.data_ptr(), _stride4(k), v.data_ptr(), _stride4(v),
+                  O.data_ptr(), _stride4(O), dO.data_ptr(), _stride4(dO), L.data_ptr(),
+                  dq.data_ptr(), _stride4(dq), dk.data_ptr(), _stride4(dk), dv.data_ptr(), _stride4(dv),
+                  ws.data_ptr())
+        return dq, dk, dv
+    # inside a training step: the same three kernels (attention.py:116, then the
+    # dK/dV and dQ kernels), with dQ on a second stream beside dK/dV
+    c = int(bool(causal))
+    _lib.call("nl_flash_attention_bwd_preprocess", _stream(q), B, H, S, D, O.data_ptr(), _stride4(O),
+              dO.data_ptr(), _stride4(dO), ws.data_ptr())
+    common = (scale, c, q.data_ptr(), _stride4(q), k.data_ptr(), _stride4(k), v.data_ptr(), _stride4(v),
+              dO.data_ptr(), _stride4(dO), L.data_ptr(), ws.data_ptr())
+    wgrad.split(
+        lambda: _lib.call("nl_flash_attention_bwd_dkdv", _stream(q), B, H, S, D, *common,
+                          dk.data_ptr(), _stride4(dk), dv.data_ptr(), _stride4(dv)),
+        lambda: _lib.call("nl_flash_attention_bwd_dq", _stream(q), B, H, S, D, *common, dq.data_ptr(),
+                          _stride4(dq)),
+        q, k, v, dO, L, ws, dq)
     return dq, dk, dv
 
 

@@ -29,23 +29,43 @@ import contextlib
 
 import torch
 
-_side: dict = {}        # device index -> side stream
+_side: dict = {}        # (device index, slot) -> stream; slot 0: weight gradients, 1: within one op
 _active: dict | None = None
 
 
-def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+def _side_stream(dev: torch.device, slot: int = 0) -> torch.cuda.Stream:
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    s = _side.get(idx)
+    s = _side.get((idx, slot))
     if s is None:
         s = torch.cuda.Stream(device=idx)  # default priority
-        _side[idx] = s
+        _side[(idx, slot)] = s
     return s
 
 
 def prepare(device=None) -> None:
-    """Create the device's side stream now (e.g. before a graph capture)."""
+    """Create the device's side streams now (e.g. before a graph capture)."""
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    _side_stream(dev)
+    _side_stream(dev, 0)
+    _side_stream(dev, 1)
+
+
+def split(first, second, *keep) -> None:
+    """Run ``first()`` on the current stream and ``second()`` (which must not
+    allocate) on the op-internal side stream, concurrently when overlapping is
+    active, and join before returning: the current stream then waits for
+    both. ``keep``: every tensor ``second`` touches (referenced until here)."""
+    if _active is None:
+        first()
+        second()
+        return
+    main = torch.cuda.current_stream()
+    aux = _side_stream(_active["dev"], 1)
+    aux.wait_stream(main)
+    with torch.cuda.stream(aux):
+        second()
+    first()
+    main.wait_stream(aux)
+    del keep
 
 
 def active() -> bool:
@@ -60,7 +80,8 @@ def overlap_weight_grads(device=None):
     if _active is not None:
         raise RuntimeError("overlap_weight_grads() does not nest")
     dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    _active = {"side": _side_stream(dev), "keep": [], "main": torch.cuda.current_stream(dev), "forked": False}
+    _active = {"side": _side_stream(dev), "keep": [], "main": torch.cuda.current_stream(dev), "forked": False,
+               "dev": dev}
     try:
         yield
     finally:
