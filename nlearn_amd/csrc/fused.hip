@@ -67,14 +67,23 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, in
   const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int64_t off = (int64_t)row * D;
-  u32x4 xv[VPL];
+  // every load of the row (x, r, gamma, beta) is issued before the first use
+  u32x4 xv[VPL], rv[VPL];
   load_row<VPL>(xv, x + off, D, lane);
+  if (r) load_row<VPL>(rv, r + off, D, lane);
+  float gg[VPL][8], bb[VPL][8];
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = (i * 64 + lane) * 8;
+    if (c < D) {
+      load8f(gamma + c, gg[i]);
+      load8f(beta + c, bb[i]);
+    }
+  }
   float f[VPL][8];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) unpack8(xv[i], f[i]);
   if (r) {
-    u32x4 rv[VPL];
-    load_row<VPL>(rv, r + off, D, lane);
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       float g[8];
@@ -107,11 +116,9 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, in
   for (int i = 0; i < VPL; ++i) {
     const int c = (i * 64 + lane) * 8;
     if (c >= D) continue;
-    float gg[8], bb[8], o[8];
-    load8f(gamma + c, gg);
-    load8f(beta + c, bb);
+    float o[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = (f[i][j] - mean) * rstd * gg[j] + bb[j];
+    for (int j = 0; j < 8; ++j) o[j] = (f[i][j] - mean) * rstd * gg[i][j] + bb[i][j];
     *reinterpret_cast<u32x4*>(y + off + c) = pack8(o);
   }
   if (lane == 0) {
@@ -139,12 +146,27 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
     for (int j = 0; j < 8; ++j) ag[i][j] = ab[i][j] = gam[i][j] = 0.f;
     if (c < D) load8f(gamma + c, gam[i]);
   }
-  for (int row = blockIdx.x * kRowsPerBlock + wave; row < rows; row += gridDim.x * kRowsPerBlock) {
+  // Rows are software-pipelined: the next row's dy, x, dres, mean and rstd are
+  // in flight while this row is computed and stored.
+  const int stride = gridDim.x * kRowsPerBlock;
+  int row = blockIdx.x * kRowsPerBlock + wave;
+  u32x4 dv[VPL], xv[VPL], rv[VPL];
+  float mu = 0.f, rs = 0.f;
+  auto fetch = [&](int rw, u32x4 (&d)[VPL], u32x4 (&xx)[VPL], u32x4 (&rr)[VPL], float& m, float& q) {
+    const int64_t o = (int64_t)rw * D;
+    load_row<VPL>(d, dy + o, D, lane);
+    load_row<VPL>(xx, x + o, D, lane);
+    if (dres) load_row<VPL>(rr, dres + o, D, lane);
+    m = mean_in[rw];
+    q = rstd_in[rw];
+  };
+  if (row < rows) fetch(row, dv, xv, rv, mu, rs);
+  while (row < rows) {
     const int64_t off = (int64_t)row * D;
-    u32x4 dv[VPL], xv[VPL];
-    load_row<VPL>(dv, dy + off, D, lane);
-    load_row<VPL>(xv, x + off, D, lane);
-    const float mu = mean_in[row], rs = rstd_in[row];
+    const int nxt = row + stride;
+    u32x4 dn[VPL], xn[VPL], rn[VPL];
+    float mun = 0.f, rsn = 0.f;
+    if (nxt < rows) fetch(nxt, dn, xn, rn, mun, rsn);
     float g[VPL][8], xh[VPL][8];
     float s1 = 0.f, s2 = 0.f;
 #pragma unroll
@@ -173,12 +195,21 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
       for (int j = 0; j < 8; ++j) o[j] = rs * (g[i][j] - m1 - xh[i][j] * m2);
       if (dres) {
         float rf[8];
-        unpack8(*reinterpret_cast<const u32x4*>(dres + off + c), rf);
+        unpack8(rv[i], rf);
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[j] += rf[j];
       }
       *reinterpret_cast<u32x4*>(dx + off + c) = pack8(o);
     }
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      dv[i] = dn[i];
+      xv[i] = xn[i];
+      rv[i] = rn[i];
+    }
+    mu = mun;
+    rs = rsn;
+    row = nxt;
   }
   // combine the 4 waves in wave order (deterministic), one partial row per workgroup
   for (int w = 0; w < kRowsPerBlock; ++w) {
