@@ -70,6 +70,17 @@ class KernelProbe:
             B, H, S, D = args[1:5]
             f = 2.0 * B * H * S * S * D if args[6] else 4.0 * B * H * S * S * D
             return f"flash_bwd_{B * H}x{S}x{D}", 2.5 * f, "flops"
+        # the training step launches the backward's kernels one by one (dQ on a
+        # second stream): executed products per kernel, S = QK^T and dP = dO V^T
+        # counted in both (dK/dV: S, dP, dV, dK; dQ: S, dP, dQ)
+        if name in ("nl_flash_attention_bwd_dkdv", "nl_flash_attention_bwd_dq"):
+            B, H, S, D = args[1:5]
+            f = 2.0 * B * H * S * S * D if args[6] else 4.0 * B * H * S * S * D
+            which = "dkdv" if name.endswith("dkdv") else "dq"
+            return f"flash_bwd_{which}_{B * H}x{S}x{D}", (2.0 if which == "dkdv" else 1.5) * f, "flops"
+        if name == "nl_flash_attention_bwd_preprocess":
+            B, H, S, D = args[1:5]
+            return f"flash_bwd_pre_{B * H}x{S}x{D}", 2.0 * 2 * B * H * S * D + 4.0 * B * H * S, "bytes"
         return None
 
     def __call__(self, name, args):
