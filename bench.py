@@ -197,8 +197,9 @@ def _probe_kernel_tag(name: str):
         return "gemm_NT_16384x512x50257"      # the only split product of the probe
     if "gemm" in name and "<" in name:
         args = [t.strip() for t in name.split("<", 1)[1].split(",")]
-        if len(args) >= 6:
-            layout = (args[4], args[5])
+        # gemm2_kernel<BM, BN, BKT, S, A_KMAJ, B_KMAJ, ...>, gemm_persist_kernel<A_KMAJ, B_KMAJ, ...>
+        layout = (args[0], args[1]) if "persist" in name else (args[4], args[5]) if len(args) >= 6 else None
+        if layout:
             return {("true", "false"): "gemm_NN_16384x50257x512", ("true", "true"): "gemm_NT_16384x512x50257",
                     ("false", "false"): "gemm_TN_512x50257x16384"}.get(layout)
     return None

@@ -949,6 +949,200 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent 256 x 256 kernel for short-K products without a split (the
+// LM-head forward, K = 512: 8 stages per tile, where a tile's first-stage load
+// and its 128 KB store were 30% of its time). One workgroup per CU walks its
+// tiles in order. While a tile's last stage is computed, the next tile's first
+// stage is already loading into the other buffer; the tile's stores then drain
+// while the next tile computes. On gfx9 stores count in vmcnt, so the next
+// tile's first wait is vmcnt(number of stores just issued): exact for interior
+// tiles, whose store path has no bounds branches; after an edge tile it is
+// vmcnt(0). Requires K % 128 == 0 (an even number of full stages, no tail).
+// ---------------------------------------------------------------------------
+template <bool A_KMAJ, bool B_KMAJ, typename OutT>
+__global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs g) {
+  constexpr int BM = 256, BN = 256, BKT = 64, NWV = 8;
+  constexpr int WNW = 4, WTM = 128, WTN = 64, FM = WTM / 32, FN = WTN / 32;
+  constexpr int STAGE = (BM + BN) * BKT;
+  __shared__ __attribute__((aligned(16))) uint16_t st0[STAGE];
+  __shared__ __attribute__((aligned(16))) uint16_t st1[STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WNW, wn = wave % WNW;
+  const int tiles_n = (g.N + BN - 1) / BN;
+  const int tiles_m = (g.M + BM - 1) / BM;
+  const int ntiles = tiles_m * tiles_n;
+  // XCD x (= blockIdx.x % 8, how the hardware deals workgroups) owns the
+  // contiguous logical tile range [x * per_x, (x + 1) * per_x); its workgroups
+  // take every (gridDim.x / 8)-th tile of it, so each XCD's L2 sees neighbours.
+  const int nx = gridDim.x / 8;
+  const int xcd = blockIdx.x % 8, jj = blockIdx.x / 8;
+  const int per_x = (ntiles + 7) / 8;
+  const int t_end = min(ntiles, (xcd + 1) * per_x);
+  constexpr int GM = 8;
+  const int in_group = GM * tiles_n;
+  auto decode = [&](int t, int& m0, int& n0) {
+    const int first_m = (t / in_group) * GM;
+    const int gsize = min(tiles_m - first_m, GM);
+    m0 = (first_m + (t % in_group) % gsize) * BM;
+    n0 = ((t % in_group) / gsize) * BN;
+  };
+  int t = xcd * per_x + jj;
+  if (t >= t_end) return;
+  const int nfull = g.K / BKT;  // even (K % 128 == 0)
+
+  const uint32_t a_bytes = (uint32_t)((((A_KMAJ ? (int64_t)(g.M - 1) * g.lda + g.K
+                                                : (int64_t)(g.K - 1) * g.lda + g.M) * 2) + 15) & ~(int64_t)15);
+  const uint32_t b_bytes = (uint32_t)((((B_KMAJ ? (int64_t)(g.N - 1) * g.ldb + g.K
+                                                : (int64_t)(g.K - 1) * g.ldb + g.N) * 2) + 15) & ~(int64_t)15);
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, a_bytes);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, b_bytes);
+  Dma<BM, BKT, A_KMAJ, NWV> da;
+  Dma<BN, BKT, B_KMAJ, NWV> db;
+  Frag<BM, BKT, A_KMAJ> fa[FM];
+  Frag<BN, BKT, B_KMAJ> fb[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) fa[i].init(wm * WTM + i * 32, lane);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) fb[j].init(wn * WTN + j * 32, lane);
+  float s = g.alpha;
+  if (g.alpha_dev) s *= *g.alpha_dev;
+
+  f32x16 acc[FM][FN];
+  bf16x8 af[2][FM], bfr[2][FN];
+  auto compute = [&](const uint16_t* sb) {
+    const uint16_t* As = sb;
+    const uint16_t* Bs = sb + BM * BKT;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) af[0][i] = fa[i].read(As, 0, lane);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) bfr[0][j] = fb[j].read(Bs, 0, lane);
+#pragma unroll
+    for (int ks = 0; ks < BKT / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < BKT / 16) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[cur ^ 1][i] = fa[i].read(As, ks + 1, lane);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bfr[cur ^ 1][j] = fb[j].read(Bs, ks + 1, lane);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[cur][j], af[cur][i], acc[i][j]);
+    }
+    constexpr int R = FM * (A_KMAJ ? 1 : 2) + FN * (B_KMAJ ? 1 : 2);
+    sched_stage<R, FM * FN, BKT / 16>();
+  };
+  auto issue = [&](uint16_t* sb, int k0) {
+    da.issue(ra, sb, k0, g.lda, wave);
+    db.issue(rb, sb + BM * BKT, k0, g.ldb, wave);
+  };
+  // raw barrier: the waits before it are explicit (__syncthreads would add vmcnt(0))
+  auto barrier = [&]() { asm volatile("s_barrier" ::: "memory"); };
+
+  constexpr int PITCH = 64 * (int)sizeof(OutT);  // one 32 x 64 slab per wave and store round
+  constexpr int CPR = PITCH / 16;
+  constexpr int EPC = 16 / (int)sizeof(OutT);
+  constexpr int RPI = 64 / CPR;
+  constexpr int kStores = FM * (32 / RPI);  // store instructions per wave, interior tile
+  static_assert(NWV * 32 * PITCH <= STAGE * 2, "slabs fit one stage buffer");
+  static_assert(kStores < 64, "vmcnt range");
+  const int frow = lane & 31;
+  const int g4 = (lane >> 5) * 4;
+  uint8_t* wl = reinterpret_cast<uint8_t*>(st1) + wave * (32 * PITCH);
+
+  int m0, n0;
+  decode(t, m0, n0);
+  da.init(m0, g.lda, wave, lane);
+  db.init(n0, g.ldb, wave, lane);
+  issue(st0, 0);
+  bool pend_stores = false;  // interior stores of the previous tile still in flight
+  while (true) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    const int t_next = t + nx;
+    const bool has_next = t_next < t_end;
+    int m1 = 0, n1 = 0;
+    for (int kt = 0; kt < nfull; kt += 2) {
+      if (kt == 0 && pend_stores) wait_vm<kStores>();
+      else wait_vm<0>();
+      barrier();
+      issue(st1, kt * BKT + BKT);
+      compute(st0);
+      wait_vm<0>();
+      barrier();
+      if (kt + 2 < nfull) {
+        issue(st0, (kt + 2) * BKT);
+      } else if (has_next) {
+        decode(t_next, m1, n1);
+        da.init(m1, g.lda, wave, lane);
+        db.init(n1, g.ldb, wave, lane);
+        issue(st0, 0);
+      }
+      compute(st1);
+    }
+    // epilogue: every wave done with st1 -> slabs there; st0 holds the next
+    // tile's first stage (in flight)
+    __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+    barrier();
+    const bool interior = m0 + BM <= g.M && n0 + BN <= g.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float x0 = acc[i][j][4 * q] * s, x1 = acc[i][j][4 * q + 1] * s, x2 = acc[i][j][4 * q + 2] * s,
+                      x3 = acc[i][j][4 * q + 3] * s;
+          const int c = j * 32 + q * 8 + g4;
+          if constexpr (sizeof(OutT) == 2) {
+            *reinterpret_cast<u32x2*>(wl + frow * 128 + ((((c * 2) >> 4) ^ (frow & 7)) << 4) + ((c * 2) & 15)) =
+                u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+          } else {
+            *reinterpret_cast<f32x4*>(wl + frow * 256 + ((((c * 4) >> 4) ^ (frow & 15)) << 4)) = f32x4{x0, x1, x2, x3};
+          }
+        }
+#pragma unroll
+      for (int it = 0; it < 32 / RPI; ++it) {
+        const int r = it * RPI + lane / CPR;
+        const int ch = lane % CPR;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(wl + r * PITCH + ((ch ^ (r & (CPR - 1))) << 4));
+        const int mm = m0 + wm * WTM + i * 32 + r;
+        const int n = n0 + wn * WTN + ch * EPC;
+        OutT* dst = reinterpret_cast<OutT*>(g.C) + (int64_t)mm * g.ldc + n;
+        if (interior) {
+          __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+        } else {
+          if (mm >= g.M || n >= g.N) continue;
+          if (n + EPC <= g.N) {
+            __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+          } else {
+#pragma unroll
+            for (int k = 0; k < EPC; ++k) {
+              if (n + k >= g.N) break;
+              if constexpr (sizeof(OutT) == 2) dst[k] = (OutT)(val[k >> 1] >> (16 * (k & 1)));
+              else dst[k] = __uint_as_float(val[k]);
+            }
+          }
+        }
+      }
+    }
+    if (!has_next) break;
+    pend_stores = interior;
+    t = t_next;
+    m0 = m1;
+    n0 = n1;
+  }
+}
+
 // Explicit instantiations: every (layout, output, epilogue) combination the
 // dispatcher can launch gets its host stub emitted. k-stage depth per layout:
 // 64 when both operands have the same major order (NT, TN), else 32 (see launch_cfg).
@@ -965,6 +1159,12 @@ NL_I8(NL_EPI_BIAS_GELU)
 NL_I8(NL_EPI_DGELU)
 template __global__ void gemm2_kernel<256, 128, 32, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, true, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, true, float>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, true, uint16_t>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, false, float>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, false, uint16_t>(GemmArgs);
+template __global__ void gemm_persist_kernel<false, false, float>(GemmArgs);
+template __global__ void gemm_persist_kernel<false, false, uint16_t>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, true, uint16_t, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, uint16_t, NL_EPI_NONE>(GemmArgs);
@@ -1005,6 +1205,19 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int spli
 }
 
 // Tile configuration and K split of one product (shared by the workspace query).
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 struct Plan {
   int big;     // 1: 256 x 128 tiles (the very large products), 0: 128 x 128
   int tiles;
@@ -1104,6 +1317,14 @@ void launch_cfg(GemmArgs g, const Plan& plan, hipStream_t st) {
   auto launch2 = [&](int grid) {
     if constexpr (AK || !BK_) {
       if (p.big == 2) {
+        // short-K products without a split: one persistent workgroup per CU
+        if (!g.ws && g.beta == 0.f && g.K % 128 == 0 && g.K <= 4096) {
+          const int cus = cu_count();
+          const int ntiles = (int)((int64_t)((g.M + 255) / 256) * ((g.N + 255) / 256));
+          const int G = std::max(8, std::min(cus / 8 * 8, (ntiles + 7) / 8 * 8));
+          hipLaunchKernelGGL((gemm_persist_kernel<AK, BK_, OutT>), dim3(G), dim3(512), 0, st, g);
+          return;
+        }
         hipLaunchKernelGGL((gemm2_kernel<256, 256, 64, 2, AK, BK_, OutT, NL_EPI_NONE>), dim3(grid), dim3(512), 0, st, g);
         return;
       }

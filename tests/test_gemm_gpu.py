@@ -160,13 +160,17 @@ def test_gemm_split_k_matches_single_pass_and_is_deterministic(dev, M, N, K):
 
 
 @pytest.mark.parametrize("opA,opB,M,N,K,out", [("N", "N", 2000, 9000, 3000, "f32"), ("N", "T", 4000, 600, 25000, "f32"),
-                                                ("T", "N", 600, 9000, 10000, "f32"), ("N", "N", 2000, 9000, 3000, "bf16")])
+                                                ("T", "N", 600, 9000, 10000, "f32"), ("N", "N", 2000, 9000, 3000, "bf16"),
+                                                ("N", "N", 4000, 12000, 1152, "bf16"), ("N", "N", 4000, 12000, 1152, "f32"),
+                                                ("N", "T", 4000, 12000, 1152, "bf16"), ("T", "N", 4000, 12000, 1152, "f32")])
 def test_gemm_huge_tile_path_exact_small_integers(dev, opA, opB, M, N, K, out):
     """Products of >= 100 GFLOP take the 256 x 256 tile path (8 waves; split K
-    for short grids: NT here splits 5 ways, TN 2 ways). Ragged M, N and K (a
-    masked k tail), checked exactly on integer inputs (every partial sum is an
-    integer below 2^24, so fp32 accumulation is exact in any order and bf16
-    output is the single rounding of the exact value)."""
+    for short grids: NT here splits 5 ways, TN 2 ways). With K % 128 == 0,
+    K <= 4096 and no split (the 1152-deep cases) the persistent variant runs:
+    one workgroup per CU over many tiles, interior and edge tiles mixed.
+    Ragged M, N and K (a masked k tail), checked exactly on integer inputs
+    (every partial sum is an integer below 2^24, so fp32 accumulation is exact
+    in any order and bf16 output is the single rounding of the exact value)."""
     import torch
     from nlearn_amd.kernels.gemm import gemm_raw
 
