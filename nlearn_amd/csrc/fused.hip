@@ -231,26 +231,56 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
   }
 }
 
-// out[c] (+)= sum_{p<P} part[p][c], summed in a fixed order: thread group ty
-// takes p = ty, ty+16, ..., then the 16 group sums are added in ty order.
-// Block: 64 columns x 16 groups.
-__global__ __launch_bounds__(1024) void sum_partials_kernel(int P, int D, const float* __restrict__ part,
-                                                            float* __restrict__ out, int accumulate) {
-  __shared__ float s[16][64];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int c = blockIdx.x * 64 + tx;
-  float a = 0.f;
-  if (c < D) {
-#pragma unroll 8
-    for (int p = ty; p < P; p += 16) a += part[(int64_t)p * D + c];
-  }
-  s[ty][tx] = a;
-  __syncthreads();
-  if (ty == 0 && c < D) {
-    float t = 0.f;
+// out[c] (+)= sum_{p<P} part[p][c] for one or two (part, out) pairs
+// (blockIdx.y picks the pair), summed in a fixed order. A workgroup owns 16
+// columns: thread (ph, q), ph < 64, q < 4, sums rows p = ph, ph+64, ... of
+// columns [4q, 4q+4) of its strip; the 64 phase sums are then added in groups
+// of 4 (phases 4g..4g+3) and the 16 group sums in g order. The strips are
+// narrow so that a 512-column sum still spreads over 32 workgroups per pair
+// with every row load in flight at once (P <= 1024: 16 loads a thread).
+__global__ __launch_bounds__(256) void sum_partials_kernel(int P, int D, const float* __restrict__ part0,
+                                                           float* __restrict__ out0, const float* __restrict__ part1,
+                                                           float* __restrict__ out1, int accumulate) {
+  __shared__ float s[64][17];
+  __shared__ float s2[16][17];
+  const float* __restrict__ part = blockIdx.y ? part1 : part0;
+  float* __restrict__ out = blockIdx.y ? out1 : out0;
+  const int q = threadIdx.x & 3, ph = threadIdx.x >> 2;
+  const int c = blockIdx.x * 16 + q * 4;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((D & 3) == 0) {
+    if (c < D) {
+#pragma unroll 16
+      for (int p = ph; p < P; p += 64) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)p * D + c);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) t += s[k][tx];
-    out[c] = accumulate ? out[c] + t : t;
+        for (int j = 0; j < 4; ++j) a[j] += v[j];
+      }
+    }
+  } else {
+#pragma unroll 4
+    for (int p = ph; p < P; p += 64) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c + j < D) a[j] += part[(int64_t)p * D + c + j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s[ph][q * 4 + j] = a[j];
+  __syncthreads();
+  {
+    const int col = threadIdx.x & 15, g = threadIdx.x >> 4;
+    s2[g][col] = ((s[4 * g][col] + s[4 * g + 1][col]) + s[4 * g + 2][col]) + s[4 * g + 3][col];
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int cc = blockIdx.x * 16 + threadIdx.x;
+    if (cc < D) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < 16; ++g) t += s2[g][threadIdx.x];
+      out[cc] = accumulate ? out[cc] + t : t;
+    }
   }
 }
 
@@ -403,9 +433,8 @@ extern "C" int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy
     NL_LNB(8)
 #undef NL_LNB
   }
-  const dim3 rg((D + 63) / 64);
-  hipLaunchKernelGGL(sum_partials_kernel, rg, dim3(1024), 0, st, blocks, D, (const float*)pg, dgamma, accumulate);
-  hipLaunchKernelGGL(sum_partials_kernel, rg, dim3(1024), 0, st, blocks, D, (const float*)pb, dbeta, accumulate);
+  hipLaunchKernelGGL(sum_partials_kernel, dim3((D + 15) / 16, 2), dim3(256), 0, st, blocks, D, (const float*)pg,
+                     dgamma, (const float*)pb, dbeta, accumulate);
   return nl_check_launch("nl_layernorm_bwd");
 }
 
@@ -428,8 +457,8 @@ extern "C" int nl_colsum_bf16(void* stream, int rows, int cols, const nl_bf16* x
   float* part = static_cast<float*>(ws);
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(colsum_partial_kernel, dim3((cols + 511) / 512, P), dim3(256), 0, st, rows, cols, x, ld, part);
-  hipLaunchKernelGGL(sum_partials_kernel, dim3((cols + 63) / 64), dim3(1024), 0, st, P, cols, (const float*)part, out,
-                     accumulate);
+  hipLaunchKernelGGL(sum_partials_kernel, dim3((cols + 15) / 16, 1), dim3(256), 0, st, P, cols, (const float*)part, out,
+                     (const float*)nullptr, (float*)nullptr, accumulate);
   return nl_check_launch("nl_colsum_bf16");
 }
 
