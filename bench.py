@@ -35,6 +35,8 @@ def _args():
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
+    ap.add_argument("--fused-lmhead", action="store_true",
+                    help="the loss through linear_cross_entropy (no logits kept between forward and backward)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the LM-head GEMM and a 1 GiB copy (for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline sample")
@@ -62,6 +64,12 @@ class KernelProbe:
         if name == "nl_ce_fwd_bwd":
             M, V = args[1:3]
             return f"ce_fwd_bwd_{M}x{V}", 4.0 * M * V + 12.0 * M, "bytes"
+        if name == "nl_lce_fwd":
+            M, D, V = args[1:4]
+            return f"lce_fwd_{M}x{V}x{D}", 2.0 * M * V * D, "flops"
+        if name == "nl_lce_bwd_dlogits":
+            M, D, V, _, vn = args[1:6]
+            return f"lce_dlogits_{M}x{vn}x{D}", 2.0 * M * vn * D, "flops"
         if name == "nl_flash_attention_fwd":
             B, H, S, D = args[1:5]
             f = 2.0 * B * H * S * S * D if args[6] else 4.0 * B * H * S * S * D
@@ -299,7 +307,7 @@ def main():
     graph = not a.no_graph
     probe = KernelProbe(torch)
     _lib.set_probe(probe)
-    step = make_train_step(opt, cfg, graph=graph, warmup=2)
+    step = make_train_step(opt, cfg, graph=graph, warmup=2, fused_lmhead=a.fused_lmhead)
     data = SyntheticTokens(bs, seq, cfg.vocab_size, seed=0, device=dev)
     batches = [data.get_batch() for _ in range(4)]
 
@@ -321,7 +329,7 @@ def main():
         # replayed graph (torch-ROCm refuses external events in a capture), so
         # the same step runs a.steps more times eagerly, every kernel bracketed
         # by events on its launch stream; kernels and shapes are identical.
-        eager = make_train_step(opt, cfg, graph=False)
+        eager = make_train_step(opt, cfg, graph=False, fused_lmhead=a.fused_lmhead)
         probe.enabled = True
         for i in range(a.steps):
             params, state, loss = eager(params, state, batches[i % 4])
@@ -357,7 +365,8 @@ def main():
         "data": "synthetic uniform tokens, random-init weights (seeded)",
         "config": {"workload": f"train_step fwd+bwd+AdamW d512/8h/4L vocab50257 bs{bs} seq{seq}",
                    "global_batch": bs, "seq_len": seq, "parallelism": "single-gpu",
-                   "launch": "hip_graph" if graph else "eager"},
+                   "launch": "hip_graph" if graph else "eager",
+                   "loss": "linear_cross_entropy" if a.fused_lmhead else "linear+cross_entropy"},
         "roofline": roof,
         "cpu_baseline": None,
         "detail": {

@@ -235,6 +235,34 @@ int nl_ce_fwd_bwd(void* stream, int M, int V,
                   float* loss, float* lse, float scale,
                   nl_bf16* dlogits, int64_t ld_dlogits);
 
+/* Fused LM head + cross-entropy: the CE of logits = X[M][D] . W[D][V] without
+ * the (M, V) logits in memory. Replaces linear_cross_entropy
+ * (cross_entropy.py:84-170, selected by NLEARN_FUSED_LMHEAD=1 in
+ * train.py:24-28,279-283), which chunks the vocabulary and recomputes each
+ * chunk's logits in the backward. X and W are bf16, row-major, 16-byte aligned
+ * with ldx, ldw multiples of 8; the logits both entry points work from are
+ * l = bf16(X . W) with fp32 accumulation, the values nl_gemm would store.
+ *
+ * nl_lce_fwd: loss[m] = lse[m] - l[m, t[m]], lse[m] = logsumexp_v l[m, v]
+ * (NaN loss for a target outside [0, V)). The GEMM reduces each 256-column
+ * tile of logits to per-row (max, sum) partials in its epilogue; a second
+ * kernel merges them. Workspace: nl_lce_ws_bytes(M, V) bytes, 16-byte aligned. */
+size_t nl_lce_ws_bytes(int M, int V);
+int nl_lce_fwd(void* stream, int M, int D, int V, const nl_bf16* X, int64_t ldx,
+               const nl_bf16* W, int64_t ldw, const int32_t* targets,
+               float* loss, float* lse, void* ws, size_t ws_bytes);
+
+/* dlogits[m][c] = (exp(l[m, v] - lse[m]) - [v == t[m]]) * scale * (*scale_dev)
+ * for vocabulary columns v = v0 + c, c < vn (scale_dev may be NULL: factor 1),
+ * written as bf16 [M][ld_dlogits]; v0 % 8 == 0 and v0 + vn <= V. The logits
+ * are recomputed by the GEMM (cross_entropy.py:150-152) and never stored. The
+ * caller forms dX = dlogits . W[:, v0:v0+vn]^T and dW[:, v0:v0+vn] =
+ * X^T . dlogits with nl_gemm (cross_entropy.py:157-158). */
+int nl_lce_bwd_dlogits(void* stream, int M, int D, int V, int v0, int vn,
+                       const nl_bf16* X, int64_t ldx, const nl_bf16* W, int64_t ldw,
+                       const int32_t* targets, const float* lse, float scale,
+                       const float* scale_dev, nl_bf16* dlogits, int64_t ld_dlogits);
+
 /* out[0] = mean(x[0..n)) in a fixed summation order (deterministic).
  * Replaces loss.mean() (cross_entropy.py:51). */
 int nl_mean_f32(void* stream, const float* x, int n, float* out);

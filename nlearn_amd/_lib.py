@@ -64,6 +64,9 @@ _SIGNATURES = {
     "nl_ce_fwd": [_P, _I, _I, _P, _I64, _P, _P, _P],
     "nl_ce_bwd": [_P, _I, _I, _P, _I64, _P, _P, _F, _P, _I64],
     "nl_ce_fwd_bwd": [_P, _I, _I, _P, _I64, _P, _P, _P, _F, _P, _I64],
+    "nl_lce_ws_bytes": [_I, _I],
+    "nl_lce_fwd": [_P, _I, _I, _I, _P, _I64, _P, _I64, _P, _P, _P, _P, ctypes.c_size_t],
+    "nl_lce_bwd_dlogits": [_P, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P, _P, _F, _P, _P, _I64],
     "nl_mean_f32": [_P, _P, _I, _P],
     "nl_scale_bf16_by_device_scalar": [_P, _P, _I64, _I64, _I64, _P],
     "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F],
@@ -86,6 +89,7 @@ _RESTYPES = {
     "nl_layernorm_bwd_ws_bytes": ctypes.c_size_t,
     "nl_adamw_multi_prepare": ctypes.c_int64,
     "nl_colsum_ws_bytes": ctypes.c_size_t,
+    "nl_lce_ws_bytes": ctypes.c_size_t,
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -59,7 +59,26 @@ struct GemmArgs {
   const float* bias;
   uint16_t* aux;
   int64_t ldaux;
+  // cross-entropy epilogues of the fused LM head (kEpiCeStats, kEpiCeGrad):
+  // column n of the product is vocabulary entry ce_v0 + n.
+  const int32_t* ce_tgt;   // targets [M]
+  const float* ce_lse;     // logsumexp [M] (gradient)
+  float* ce_part;          // per-row, per-tile (max, sum) partials [M][tiles_n] (statistics)
+  float* ce_correct;       // the target's logit [M] (statistics)
+  int ce_v0;
+  float ce_scale;          // gradient scale (times *ce_scale_dev when given)
+  const float* ce_scale_dev;
 };
+
+// Epilogues of the fused LM head + cross-entropy (internal; not NL_EPI_* values).
+// Both see the logits l = bf16(alpha * s * acc), the values the unfused path
+// stores and the CE kernel reads.
+//   kEpiCeStats: nothing is stored; each row of a tile yields (max, sum of
+//                2^(l*log2e - max)) over the tile's columns and, from the
+//                tile holding it, the target's logit.
+//   kEpiCeGrad:  C = bf16((exp(l - lse[m]) - [v0 + n == t[m]]) * scale).
+constexpr int kEpiCeStats = 16;
+constexpr int kEpiCeGrad = 17;
 
 __device__ __forceinline__ int swz(int row, int kc) { return (kc ^ ((row ^ (row >> 3)) & 7)); }
 
@@ -584,6 +603,15 @@ __device__ __forceinline__ void sched_stage() {
   }
 }
 
+// Merge (max, sum of 2^(x - max)) partials, both in log2 units; an empty
+// partial is (-inf, 0).
+__device__ __forceinline__ void ce_combine(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * fast_exp2(m - mn) + s2 * fast_exp2(m2 - mn);
+  m = mn;
+}
+
 // wait until at most `later` stages (IPS DMA ops each) of this wave are outstanding
 template <int IPS, int MAXL>
 __device__ __forceinline__ void wait_stage(int later) {
@@ -686,7 +714,7 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   bf16x8 af[2][FM], bfr[2][FN];
-  auto compute = [&](const uint16_t* sb) {
+  auto compute = [&](const uint16_t* sb) __attribute__((always_inline)) {
     const uint16_t* As = sb;
     const uint16_t* Bs = sb + BM * BKT;
 #pragma unroll
@@ -713,7 +741,7 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
       sched_stage<R, FM * FN, BKT / 16>();
     }
   };
-  auto issue = [&](uint16_t* sb, int st) {  // DMA of full stage st (0-based within this split)
+  auto issue = [&](uint16_t* sb, int st) __attribute__((always_inline)) {  // DMA of stage st (0-based in this split)
     const int k0 = kbeg + st * BKT;
     da.issue(ra, sb, k0, g.lda, wave);
     db.issue(rb, sb + BM * BKT, k0, g.ldb, wave);
@@ -726,7 +754,7 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   // stage kt-1, compute stage kt. With three stages the barrier is a bare
   // s_barrier (a memory clobber for the compiler): __syncthreads would also
   // wait for the DMA still in flight.
-  auto step = [&](uint16_t* cur, uint16_t* nxt, int kt) {
+  auto step = [&](uint16_t* cur, uint16_t* nxt, int kt) __attribute__((always_inline)) {
     wait_stage<IPS, S - 2>(min(S - 2, nfull - 1 - kt));
     if constexpr (S == 2) __syncthreads();
     else asm volatile("s_barrier" ::: "memory");
@@ -761,6 +789,93 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   }
   const int frow = lane & 31;
   const int g4 = (lane >> 5) * 4;
+  if constexpr (EPI == kEpiCeStats) {
+    // Lane (frow, g4) holds row frow of each 32-row block and 16 of every 32
+    // columns; lanes l and l ^ 32 share a row. Per row: the wave's (max, sum)
+    // over its WTN columns, then the WNW waves of a row band merged in LDS.
+    // Logits are rounded in pairs (one v_cvt_pk_bf16_f32); column bounds are
+    // checked only in the wave tile that crosses N, and the target's logit is
+    // looked for only by lanes whose row's target lies in the wave tile.
+    float s = g.alpha;
+    if (g.alpha_dev) s *= *g.alpha_dev;
+    static_assert(STAGE * 2 >= WNW * BM * 8, "row partials of all wave columns fit the first stage buffer");
+    float2* red = reinterpret_cast<float2*>(st0);  // [WNW][BM]
+    const int wc0 = n0 + wn * WTN;                  // first column of the wave tile
+    const int nlim = g.N - wc0;                     // its valid columns (may be <= 0)
+    const bool full = nlim >= WTN;
+    __syncthreads();                                // every wave is done reading the stage buffers
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int ml = wm * WTM + i * 32 + frow;
+      const int m = m0 + ml;
+      const int tc = (m < g.M ? g.ce_tgt[m] - g.ce_v0 : -1) - wc0;
+      uint32_t pk[FN][8];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int h = 0; h < 8; ++h) pk[j][h] = pack_bf16x2(acc[i][j][2 * h] * s, acc[i][j][2 * h + 1] * s);
+      // element 2h + b of pk[j] is column j*32 + (h >> 1)*8 + g4 + (h & 1)*2 + b
+      auto col = [&](int j, int h, int b) { return j * 32 + (h >> 1) * 8 + g4 + (h & 1) * 2 + b; };
+      float mx = -INFINITY;
+      if (full) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int h = 0; h < 8; ++h) mx = fmaxf(mx, fmaxf(bf16_lo(pk[j][h]), bf16_hi(pk[j][h])));
+      } else {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int h = 0; h < 8; ++h) {
+            if (col(j, h, 0) < nlim) mx = fmaxf(mx, bf16_lo(pk[j][h]));
+            if (col(j, h, 1) < nlim) mx = fmaxf(mx, bf16_hi(pk[j][h]));
+          }
+      }
+      if ((unsigned)tc < (unsigned)WTN) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int h = 0; h < 8; ++h) {
+            if (col(j, h, 0) == tc) g.ce_correct[m] = bf16_lo(pk[j][h]);
+            if (col(j, h, 1) == tc) g.ce_correct[m] = bf16_hi(pk[j][h]);
+          }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float mx2 = mx * kLog2e;
+      float sum = 0.f;
+      if (full) {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int h = 0; h < 8; ++h)
+            sum += fast_exp2(__builtin_fmaf(bf16_lo(pk[j][h]), kLog2e, -mx2)) +
+                   fast_exp2(__builtin_fmaf(bf16_hi(pk[j][h]), kLog2e, -mx2));
+      } else {
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int h = 0; h < 8; ++h) {
+            if (col(j, h, 0) < nlim) sum += fast_exp2(__builtin_fmaf(bf16_lo(pk[j][h]), kLog2e, -mx2));
+            if (col(j, h, 1) < nlim) sum += fast_exp2(__builtin_fmaf(bf16_hi(pk[j][h]), kLog2e, -mx2));
+          }
+      }
+      sum += __shfl_xor(sum, 32, 64);
+      if (lane < 32) red[wn * BM + ml] = make_float2(mx2, sum);
+    }
+    __syncthreads();
+    for (int r = tid; r < BM; r += NT) {
+      const int m = m0 + r;
+      if (m >= g.M) break;
+      float pm = -INFINITY, ps = 0.f;
+#pragma unroll
+      for (int w = 0; w < WNW; ++w) {
+        const float2 v = red[w * BM + r];
+        ce_combine(pm, ps, v.x, v.y);
+      }
+      reinterpret_cast<float2*>(g.ce_part)[(int64_t)m * tiles_n + tn] = make_float2(pm, ps);
+    }
+    return;
+  }
   if (g.ws) {
     float* W = g.ws + (int64_t)split * g.M * g.ldw;
 #pragma unroll
@@ -813,7 +928,8 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   }
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
-  if (g.beta != 0.f) {
+  constexpr bool kCeGrad = EPI == kEpiCeGrad;
+  if (!kCeGrad && g.beta != 0.f) {
     // C is read back: per-lane path (the reads sit between the stores)
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -845,10 +961,26 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   // by row, and reads it back so that consecutive lanes hold consecutive
   // 16-byte pieces of a row. Values are finished (scale, bias, GELU') group by
   // group on the way into LDS, which keeps few of them live in VGPRs.
-  static_assert(WTN == 64, "the store transpose assumes 64-column wave tiles");
-  static_assert(STAGE * 2 >= NWV / 2 * 8192, "an 8 KB slab per wave in the first two stage buffers");
-  uint8_t* wl = kAuxInSt1 ? reinterpret_cast<uint8_t*>(st0) + wave * 8192
-                          : reinterpret_cast<uint8_t*>(wave < NWV / 2 ? st0 : st1) + (wave % (NWV / 2)) * 8192;
+  // A slab row holds the wave tile's WTN columns: CPR 16-byte chunks, chunk c
+  // of row r at slot c ^ (r & (CPR - 1)).
+  constexpr int SLAB = 32 * WTN * (int)sizeof(OutT);
+  static_assert(STAGE * 2 >= NWV / 2 * SLAB, "a slab per wave in the first two stage buffers");
+  static_assert(!kAuxInSt1 || NWV * SLAB <= STAGE * 2, "slabs and the aux tile share no bytes");
+  uint8_t* wl = kAuxInSt1 ? reinterpret_cast<uint8_t*>(st0) + wave * SLAB
+                          : reinterpret_cast<uint8_t*>(wave < NWV / 2 ? st0 : st1) + (wave % (NWV / 2)) * SLAB;
+  // cross-entropy gradient: each lane's rows' lse (log2 units) and target column
+  float ce_l2[FM];
+  int ce_t[FM];
+  float ce_gs = 0.f;
+  if constexpr (kCeGrad) {
+    ce_gs = g.ce_scale * (g.ce_scale_dev ? *g.ce_scale_dev : 1.f);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int m = m0 + wm * WTM + i * 32 + frow;
+      ce_l2[i] = m < g.M ? g.ce_lse[m] * kLog2e : 0.f;
+      ce_t[i] = m < g.M ? g.ce_tgt[m] - g.ce_v0 - n0 : -1;
+    }
+  }
   auto finish4 = [&](int i, int j, int q, float x[4]) {
     const int nl = wn * WTN + j * 32 + q * 8 + g4;
     f32x4 b = {0.f, 0.f, 0.f, 0.f};
@@ -864,18 +996,31 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
       if constexpr (kBias) x[e] += b[e];
       if constexpr (kAux) x[e] *= gelu_tanh_grad(e & 1 ? bf16_hi(a[e >> 1]) : bf16_lo(a[e >> 1]));
     }
+    if constexpr (kCeGrad) {
+      // the logits as bf16 (one packed conversion per pair), then the CE gradient
+      const uint32_t p01 = pack_bf16x2(x[0], x[1]), p23 = pack_bf16x2(x[2], x[3]);
+      const float l[4] = {bf16_lo(p01), bf16_hi(p01), bf16_lo(p23), bf16_hi(p23)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = fast_exp2(__builtin_fmaf(l[e], kLog2e, -ce_l2[i]));
+        x[e] = (nl + e == ce_t[i] ? p - 1.f : p) * ce_gs;
+      }
+    }
   };
   // write the lane's 4 values of (slab row frow, columns j*32 + q*8 + g4 ..) into the slab
   auto at_bf16 = [&](int j, int q) {
-    const int c = j * 32 + q * 8 + g4;                  // 128-byte rows, 8 chunks
-    return reinterpret_cast<u32x2*>(wl + frow * 128 + ((((c * 2) >> 4) ^ (frow & 7)) << 4) + ((c * 2) & 15));
+    constexpr int CPR = WTN * 2 / 16;                   // WTN * 2-byte rows
+    const int c = j * 32 + q * 8 + g4;
+    return reinterpret_cast<u32x2*>(wl + frow * (WTN * 2) + ((((c * 2) >> 4) ^ (frow & (CPR - 1))) << 4) + ((c * 2) & 15));
   };
   auto put_bf16 = [&](int j, int q, const float x[4]) {
     *at_bf16(j, q) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
   };
   auto put_f32 = [&](int j, int q, const float x[4]) {
-    const int c = j * 32 + q * 8 + g4;                  // 256-byte rows, 16 chunks
-    *reinterpret_cast<f32x4*>(wl + frow * 256 + ((((c * 4) >> 4) ^ (frow & 15)) << 4)) = f32x4{x[0], x[1], x[2], x[3]};
+    constexpr int CPR = WTN * 4 / 16;                   // WTN * 4-byte rows
+    const int c = j * 32 + q * 8 + g4;
+    *reinterpret_cast<f32x4*>(wl + frow * (WTN * 4) + ((((c * 4) >> 4) ^ (frow & (CPR - 1))) << 4)) =
+        f32x4{x[0], x[1], x[2], x[3]};
   };
   // copy slab i (32 rows) from LDS to global rows, 16 bytes per lane
   auto copy_out = [&](auto tag, int i, void* base, int64_t ld) {
@@ -1013,7 +1158,7 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs g) {
 
   f32x16 acc[FM][FN];
   bf16x8 af[2][FM], bfr[2][FN];
-  auto compute = [&](const uint16_t* sb) {
+  auto compute = [&](const uint16_t* sb) __attribute__((always_inline)) {
     const uint16_t* As = sb;
     const uint16_t* Bs = sb + BM * BKT;
 #pragma unroll
@@ -1158,6 +1303,8 @@ NL_I8(NL_EPI_BIAS)
 NL_I8(NL_EPI_BIAS_GELU)
 NL_I8(NL_EPI_DGELU)
 template __global__ void gemm2_kernel<256, 128, 32, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, uint16_t, kEpiCeStats>(GemmArgs);
+template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, uint16_t, kEpiCeGrad>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, true, float, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm_persist_kernel<true, true, float>(GemmArgs);
 template __global__ void gemm_persist_kernel<true, true, uint16_t>(GemmArgs);
@@ -1386,10 +1533,129 @@ void launch_typed(int opA, int opB, const GemmArgs& g, const Plan& p, hipStream_
   else launch_layout<false, true, OutT>(g, p, st);
 }
 
+// ---------------------------------------------------------------------------
+// Fused LM head + cross-entropy (linear_cross_entropy)
+// ---------------------------------------------------------------------------
+
+constexpr int kLceTile = 256;  // the 256 x 256 tiles of the LM-head GEMM
+
+int lce_tiles_n(int V) { return (V + kLceTile - 1) / kLceTile; }
+
+// Per row: merge the tiles' (max, sum) partials into lse; loss = lse - the
+// target's logit (NaN for a target outside [0, V)). One wave per row.
+__global__ __launch_bounds__(256) void lce_merge_kernel(int M, int V, int tiles_n, const float2* __restrict__ part,
+                                                        const float* __restrict__ correct,
+                                                        const int32_t* __restrict__ tgt, float* __restrict__ loss,
+                                                        float* __restrict__ lse) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  float pm = -INFINITY, ps = 0.f;
+  for (int k = lane; k < tiles_n; k += 64) {
+    const float2 v = part[(int64_t)row * tiles_n + k];
+    ce_combine(pm, ps, v.x, v.y);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float m2 = __shfl_xor(pm, o, 64), s2 = __shfl_xor(ps, o, 64);
+    ce_combine(pm, ps, m2, s2);
+  }
+  if (lane == 0) {
+    const float l = (pm + fast_log2(ps)) * kLn2;
+    const int t = tgt[row];
+    lse[row] = l;
+    loss[row] = (t >= 0 && t < V) ? l - correct[row] : __builtin_nanf("");
+  }
+}
+
+// One launch of the 256 x 256 NN kernel over X[M][D] . W[D][vn] with a CE epilogue.
+template <int EPI>
+void launch_lce(GemmArgs g, hipStream_t st) {
+  g.tiles = (int)((int64_t)((g.M + kLceTile - 1) / kLceTile) * lce_tiles_n(g.N));
+  g.k_chunk = g.K;
+  g.ws = nullptr;
+  hipLaunchKernelGGL((gemm2_kernel<kLceTile, kLceTile, 64, 2, true, false, uint16_t, EPI>), dim3(g.tiles), dim3(512),
+                     0, st, g);
+}
+
+int check_lce_args(int M, int D, int V, const void* X, int64_t ldx, const void* W, int64_t ldw, const void* tgt) {
+  if (M < 0 || D <= 0 || V <= 0) return nl_set_error(NL_EINVAL, "lce: need M >= 0, D > 0, V > 0");
+  if (M > 0 && (!X || !W || !tgt)) return nl_set_error(NL_EINVAL, "lce: null pointer");
+  if (ldx < D || ldw < V) return nl_set_error(NL_EINVAL, "lce: leading dimension too small");
+  if ((((uintptr_t)X | (uintptr_t)W) & 15) != 0 || ((ldx | ldw) & 7) != 0)
+    return nl_set_error(NL_EALIGN, "lce: X and W 16-byte aligned, ldx and ldw multiples of 8");
+  // the kernel addresses X and W with 32-bit buffer offsets (up to a tile past the end)
+  if (((int64_t)M + kLceTile) * ldx * 2 >= ((int64_t)1 << 31) || ((int64_t)D + 64) * ldw * 2 >= ((int64_t)1 << 31))
+    return nl_set_error(NL_EUNSUPPORTED, "lce: X or W larger than 2 GiB");
+  return NL_OK;
+}
+
+GemmArgs lce_args(int M, int D, int N, const nl_bf16* X, int64_t ldx, const nl_bf16* W, int64_t ldw,
+                  const int32_t* tgt, int v0) {
+  GemmArgs g{};
+  g.M = M;
+  g.N = N;
+  g.K = D;
+  g.A = X;
+  g.lda = ldx;
+  g.B = W;
+  g.ldb = ldw;
+  g.alpha = 1.f;
+  g.beta = 0.f;
+  g.ce_tgt = tgt;
+  g.ce_v0 = v0;
+  return g;
+}
+
 }  // namespace
 }  // namespace nl
 
 using namespace nl;
+
+extern "C" size_t nl_lce_ws_bytes(int M, int V) {
+  if (M <= 0 || V <= 0) return 0;
+  return (size_t)M * lce_tiles_n(V) * 2 * sizeof(float) + (size_t)M * sizeof(float);
+}
+
+extern "C" int nl_lce_fwd(void* stream, int M, int D, int V, const nl_bf16* X, int64_t ldx, const nl_bf16* W,
+                          int64_t ldw, const int32_t* targets, float* loss, float* lse, void* ws, size_t ws_bytes) {
+  int rc = check_lce_args(M, D, V, X, ldx, W, ldw, targets);
+  if (rc != NL_OK) return rc;
+  if (M == 0) return NL_OK;
+  if (!loss || !lse || !ws) return nl_set_error(NL_EINVAL, "lce_fwd: null pointer");
+  if (((uintptr_t)ws & 15) != 0) return nl_set_error(NL_EALIGN, "lce_fwd: ws must be 16-byte aligned");
+  if (ws_bytes < nl_lce_ws_bytes(M, V)) return nl_set_error(NL_EINVAL, "lce_fwd: workspace smaller than nl_lce_ws_bytes()");
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs g = lce_args(M, D, V, X, ldx, W, ldw, targets, 0);
+  const int tn = lce_tiles_n(V);
+  g.ce_part = static_cast<float*>(ws);
+  g.ce_correct = g.ce_part + (size_t)M * tn * 2;
+  launch_lce<kEpiCeStats>(g, st);
+  hipLaunchKernelGGL(lce_merge_kernel, dim3((M + 3) / 4), dim3(256), 0, st, M, V, tn,
+                     reinterpret_cast<const float2*>(g.ce_part), (const float*)g.ce_correct, targets, loss, lse);
+  return nl_check_launch("nl_lce_fwd");
+}
+
+extern "C" int nl_lce_bwd_dlogits(void* stream, int M, int D, int V, int v0, int vn, const nl_bf16* X, int64_t ldx,
+                                  const nl_bf16* W, int64_t ldw, const int32_t* targets, const float* lse,
+                                  float scale, const float* scale_dev, nl_bf16* dlogits, int64_t ld_dlogits) {
+  int rc = check_lce_args(M, D, V, X, ldx, W, ldw, targets);
+  if (rc != NL_OK) return rc;
+  if (v0 < 0 || vn < 0 || v0 > V - vn || (v0 & 7) != 0)
+    return nl_set_error(NL_EINVAL, "lce_bwd: need 0 <= v0, v0 + vn <= V and v0 % 8 == 0");
+  if (M == 0 || vn == 0) return NL_OK;
+  if (!lse || !dlogits) return nl_set_error(NL_EINVAL, "lce_bwd: null pointer");
+  if (ld_dlogits < vn || (ld_dlogits & 7) != 0 || ((uintptr_t)dlogits & 15) != 0)
+    return nl_set_error(NL_EALIGN, "lce_bwd: dlogits 16-byte aligned with ld_dlogits >= vn, a multiple of 8");
+  GemmArgs g = lce_args(M, D, vn, X, ldx, W + v0, ldw, targets, v0);
+  g.C = dlogits;
+  g.ldc = ld_dlogits;
+  g.ce_lse = lse;
+  g.ce_scale = scale;
+  g.ce_scale_dev = scale_dev;
+  launch_lce<kEpiCeGrad>(g, (hipStream_t)stream);
+  return nl_check_launch("nl_lce_bwd_dlogits");
+}
 
 extern "C" size_t nl_gemm_ws_bytes(int opA, int opB, int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;

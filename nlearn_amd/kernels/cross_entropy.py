@@ -14,13 +14,21 @@ Mirrors nlearn/kernels/cross_entropy.py:
   host synchronisation happens.
 * ``_ce_fwd_raw`` / ``_ce_bwd_raw`` keep the reference's two-target form
   (cross_entropy.py:28-46) for callers that want the separate passes.
+* ``linear_cross_entropy(X, W, targets)``: the LM head and the CE fused, with
+  no (M, V) logits in memory between forward and backward
+  (cross_entropy.py:84-170). The forward GEMM reduces its tiles of logits to
+  per-row softmax statistics in the epilogue, so the logits are never stored;
+  the backward recomputes them in a GEMM whose epilogue writes dlogits, for
+  the whole vocabulary at once or in ``NLEARN_LCE_CHUNK``-column slices.
 """
 from __future__ import annotations
+
+import os
 
 import torch
 
 from .. import _lib
-from .gemm import _check_device
+from .gemm import _check_device, _kernel_ready, bf16_shadow, gemm_raw, grad_buffer, padded_empty, weight_grad
 
 _BF16 = torch.bfloat16
 
@@ -132,3 +140,103 @@ def cross_entropy(logits: torch.Tensor, targets: torch.Tensor, inplace: bool = F
     x = _as_rows(logits)
     out = _CE.apply(x, targets, inplace)
     return out
+
+
+# ---------------------------------------------------------------------------
+# linear_cross_entropy — cross_entropy.py:84-170
+# ---------------------------------------------------------------------------
+
+# Columns of dlogits the backward forms at a time (0: the whole vocabulary).
+# The reference chunks by NLEARN_LCE_CHUNK = 4096 in both passes
+# (cross_entropy.py:93); here the forward never needs chunks, and the backward
+# only needs them to cap the transient dlogits buffer (M x chunk bf16).
+_LCE_CHUNK = int(os.environ.get("NLEARN_LCE_CHUNK", "0"))
+
+
+def _lce_chunk(V: int) -> int:
+    if _LCE_CHUNK <= 0 or _LCE_CHUNK >= V:
+        return V
+    return max(256, _LCE_CHUNK // 256 * 256)
+
+
+class _LinearCE(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x2, W, targets):
+        Wb = bf16_shadow(W)
+        xb = _kernel_ready(x2)
+        t = _targets(targets)
+        _check_device(xb, Wb, t)
+        M, D = xb.shape
+        if Wb.shape[0] != D:
+            raise ValueError(f"linear_cross_entropy: X has {D} features, W has {Wb.shape[0]} rows")
+        if t.numel() != M:
+            raise ValueError("linear_cross_entropy: one target per row of X")
+        V = Wb.shape[1]
+        loss_rows = torch.empty(M, dtype=torch.float32, device=xb.device)
+        lse = torch.empty(M, dtype=torch.float32, device=xb.device)
+        wsb = int(_lib.load().nl_lce_ws_bytes(M, V))
+        ws = torch.empty(max(wsb, 16) // 4, dtype=torch.float32, device=xb.device)
+        _lib.call("nl_lce_fwd", _stream(xb), M, D, V, xb.data_ptr(), _ld(xb), Wb.data_ptr(), _ld(Wb), t.data_ptr(),
+                  loss_rows.data_ptr(), lse.data_ptr(), ws.data_ptr(), wsb)
+        ctx.save_for_backward(xb, W, t, lse)
+        ctx.wb = Wb
+        ctx.x_dtype = x2.dtype
+        return mean(loss_rows)
+
+    @staticmethod
+    def backward(ctx, g):
+        xb, W, t, lse = ctx.saved_tensors
+        Wb = ctx.wb
+        M, D = xb.shape
+        V = Wb.shape[1]
+        g = g.reshape(1).to(torch.float32).contiguous()
+        chunk = _lce_chunk(V)
+        mg = grad_buffer(W) if ctx.needs_input_grad[1] else None
+        dX = dW = None
+
+        def dlogits(v0: int, vn: int, buf: torch.Tensor) -> torch.Tensor:
+            d = buf[:, :vn]
+            _lib.call("nl_lce_bwd_dlogits", _stream(xb), M, D, V, v0, vn, xb.data_ptr(), _ld(xb), Wb.data_ptr(),
+                      _ld(Wb), t.data_ptr(), lse.data_ptr(), 1.0 / M, g.data_ptr(), d.data_ptr(), _ld(d))
+            return d
+
+        if chunk >= V:
+            # one pass: dlogits for the whole vocabulary (freed after the two products)
+            d = dlogits(0, V, padded_empty(M, V, torch.bfloat16, xb.device))
+            if ctx.needs_input_grad[0]:
+                dX = gemm_raw(d, Wb, "N", "T", out_dtype=ctx.x_dtype)          # dlogits . W^T
+            if ctx.needs_input_grad[1]:
+                if mg is not None:
+                    weight_grad(xb, d, mg)                                       # X^T . dlogits
+                else:
+                    dW = gemm_raw(xb, d, "T", "N", out_dtype=torch.float32)
+            return dX, dW, None
+        # vocabulary slices through one reused buffer; dX accumulates in fp32.
+        # The slices run on the current stream: a forked product would still be
+        # reading the buffer when the next slice overwrites it.
+        buf = padded_empty(M, chunk, torch.bfloat16, xb.device)
+        dx32 = torch.zeros((M, D), dtype=torch.float32, device=xb.device) if ctx.needs_input_grad[0] else None
+        if ctx.needs_input_grad[1]:
+            dWt = mg if mg is not None else padded_empty(D, V, torch.float32, xb.device)
+        for v0 in range(0, V, chunk):
+            vn = min(chunk, V - v0)
+            d = dlogits(v0, vn, buf)
+            if dx32 is not None:
+                gemm_raw(d, Wb[:, v0:v0 + vn], "N", "T", out=dx32, beta=1.0)
+            if ctx.needs_input_grad[1]:
+                gemm_raw(xb, d, "T", "N", out=dWt[:, v0:v0 + vn])
+        if dx32 is not None:
+            dX = dx32.to(ctx.x_dtype)
+        if ctx.needs_input_grad[1] and mg is None:
+            dW = dWt
+        return dX, dW, None
+
+
+def linear_cross_entropy(X: torch.Tensor, W: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+    """Mean softmax CE of logits = X[M, D] @ W[D, V] against int targets[M],
+    differentiable in X and W, without materialising the (M, V) logits
+    (cross_entropy.py:119-124). X is bf16 (leading dims are flattened), W the
+    fp32 LM-head weight (its bf16 copy is what the GEMMs read)."""
+    if X.dim() < 2 or W.dim() != 2:
+        raise ValueError("linear_cross_entropy: X needs >= 2 dims and W exactly 2")
+    return _LinearCE.apply(X.reshape(-1, X.shape[-1]), W, targets.reshape(-1))

@@ -24,8 +24,9 @@ import torch
 
 from . import _lib
 from .kernels import wgrad
-from .kernels.cross_entropy import cross_entropy
-from .model import BASELINE, ModelConfig, count_params, init_model, model_forward, tree_leaves
+from .kernels.cross_entropy import cross_entropy, linear_cross_entropy
+from .model import (BASELINE, ModelConfig, count_params, init_model, model_forward, model_forward_features,
+                    output_projection, tree_leaves)
 
 WARMUP_STEPS = int(os.environ.get("NLEARN_WARMUP", "200"))
 PEAK_LR = 1e-3
@@ -38,14 +39,25 @@ BATCH_SIZE = 32
 # ---------------------------------------------------------------------------
 
 
-def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE) -> torch.Tensor:
-    """Mean CE of predicting batch[:, 1:] from batch[:, :-1] (train.py:270-285).
+# NLEARN_FUSED_LMHEAD=1 fuses the LM head and the CE (linear_cross_entropy) so
+# that the (bs*seq, vocab) logits are never materialised (train.py:24-28).
+FUSED_LMHEAD = os.environ.get("NLEARN_FUSED_LMHEAD") == "1"
 
-    The logits are only read by the CE, so its single pass writes dlogits over
-    them (inplace=True): the (bs*seq, vocab) gradient costs no extra memory.
+
+def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_lmhead: bool | None = None) -> torch.Tensor:
+    """Mean CE of predicting batch[:, 1:] from batch[:, :-1] (train.py:270-299).
+
+    Default: the logits are only read by the CE, so its single pass writes
+    dlogits over them (inplace=True): the (bs*seq, vocab) gradient costs no
+    extra memory. ``fused_lmhead`` (default: NLEARN_FUSED_LMHEAD) takes the
+    linear_cross_entropy path instead (train.py:279-283), which keeps no logits
+    between the forward and the backward and recomputes them in the backward.
     """
     input_ids = batch[:, :-1]
     target_ids = batch[:, 1:]
+    if FUSED_LMHEAD if fused_lmhead is None else fused_lmhead:
+        x = model_forward_features(params, input_ids, cfg)
+        return linear_cross_entropy(x.reshape(-1, cfg.d_model), output_projection(params), target_ids.reshape(-1))
     logits = model_forward(params, input_ids, cfg)
     return cross_entropy(logits, target_ids, inplace=True)
 
@@ -216,7 +228,7 @@ class AdamW:
 
 
 def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool = False, warmup: int = 2,
-                    overlap_wgrad: bool = True):
+                    overlap_wgrad: bool = True, fused_lmhead: bool | None = None):
     """train_step(params, opt_state, batch) -> (params, opt_state, loss).
 
     Parameters are updated in place; the loss is a 0-d device tensor (no host
@@ -229,13 +241,15 @@ def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool =
 
     overlap_wgrad: run the weight-gradient kernels on a second stream beside
     the input-gradient chain (kernels.wgrad); results are identical.
+
+    fused_lmhead: the loss through linear_cross_entropy (see ``batch_loss``).
     """
     overlap = wgrad.overlap_weight_grads if overlap_wgrad else _no_overlap
 
     def eager_step(params, opt_state, batch):
         for p in tree_leaves(params):
             p.grad = None
-        loss = batch_loss(params, batch, cfg)
+        loss = batch_loss(params, batch, cfg, fused_lmhead)
         # weight gradients run on a second stream beside the dX chain; the
         # context joins it before the optimizer reads the gradient buffers
         with overlap(loss.device):
@@ -246,7 +260,7 @@ def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool =
 
     if not graph:
         return eager_step
-    return _GraphedStep(optimizer, cfg, eager_step, warmup, overlap)
+    return _GraphedStep(optimizer, cfg, eager_step, warmup, overlap, fused_lmhead)
 
 
 @contextlib.contextmanager
@@ -255,9 +269,10 @@ def _no_overlap(device=None):
 
 
 class _GraphedStep:
-    def __init__(self, optimizer, cfg, eager_step, warmup, overlap):
+    def __init__(self, optimizer, cfg, eager_step, warmup, overlap, fused_lmhead):
         self.opt, self.cfg, self.eager_step, self.warmup = optimizer, cfg, eager_step, warmup
         self.overlap = overlap
+        self.fused_lmhead = fused_lmhead
         self.done = 0
         self.graph = None
         self.static_batch = None
@@ -274,7 +289,7 @@ class _GraphedStep:
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            loss = batch_loss(params, self.static_batch, self.cfg)
+            loss = batch_loss(params, self.static_batch, self.cfg, self.fused_lmhead)
             with self.overlap(loss.device):
                 loss.backward()
             with torch.no_grad():

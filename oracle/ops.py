@@ -134,3 +134,51 @@ def ce(logits, targets, scale=None):
     dl = np.exp(x - lse[:, None])
     dl[np.arange(M), t] -= 1.0
     return loss, lse, dl * sc
+
+
+# ---------------------------------------------------------------------------
+# fused LM head + cross-entropy — cross_entropy.py:84-170
+# ---------------------------------------------------------------------------
+
+
+def linear_ce(X, W, targets, chunk: int = 4096, round_bf16: bool = True):
+    """linear_cross_entropy with g = 1: (loss, lse, dX, dW).
+
+    Follows the reference's chunked form: the forward folds each vocabulary
+    chunk's logits into an online (max, sum) and keeps the target's logit
+    (cross_entropy.py:102-116); the backward recomputes each chunk's logits and
+    accumulates dX and the chunk's dW columns (cross_entropy.py:133-161). With
+    ``round_bf16`` the logits and dlogits are rounded to bf16 before use, as the
+    reference's bf16 matmul outputs and operands are (gemm.py:51-52, 115).
+    """
+    X = np.asarray(X, np.float64)
+    W = np.asarray(W, np.float64)
+    t = np.asarray(targets, np.int64)
+    M, D = X.shape
+    V = W.shape[1]
+    rows = np.arange(M)
+    rnd = (lambda a: bf16_round(a).astype(np.float64)) if round_bf16 else (lambda a: a)
+    run_max = np.full(M, -np.inf)
+    run_sum = np.zeros(M)
+    correct = np.zeros(M)
+    for cs in range(0, V, chunk):
+        lc = rnd(X @ W[:, cs:cs + chunk])
+        nm = np.maximum(run_max, lc.max(-1))
+        run_sum = run_sum * np.exp(run_max - nm) + np.exp(lc - nm[:, None]).sum(-1)
+        run_max = nm
+        inc = (t >= cs) & (t < cs + lc.shape[1])
+        correct[inc] = lc[rows[inc], t[inc] - cs]
+    lse = run_max + np.log(run_sum)
+    loss = float((lse - correct).mean())
+    dX = np.zeros((M, D))
+    dW = np.zeros((D, V))
+    for cs in range(0, V, chunk):
+        Wc = W[:, cs:cs + chunk]
+        lc = rnd(X @ Wc)
+        dl = np.exp(lc - lse[:, None])
+        inc = (t >= cs) & (t < cs + lc.shape[1])
+        dl[rows[inc], t[inc] - cs] -= 1.0
+        dl = rnd(dl / M)
+        dX += dl @ Wc.T
+        dW[:, cs:cs + chunk] = X.T @ dl
+    return loss, lse, dX, dW

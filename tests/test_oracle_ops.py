@@ -116,6 +116,46 @@ def test_ce_vs_torch_and_invariants():
     np.testing.assert_allclose(l0, math.log(V), rtol=1e-14)
 
 
+def test_linear_ce_oracle_pins():
+    """ops.linear_ce (the chunked restatement of linear_cross_entropy) against
+    checks that do not share its code: torch float64 autograd of
+    CE(X @ W) for the loss and both gradients (unrounded), chunk-size
+    independence (a wrong online rescale would break it), and W = 0, where the
+    loss is exactly ln V and dW = X^T (1/V - onehot) / M."""
+    rng = np.random.default_rng(11)
+    M, D, V = 13, 7, 50
+    X = rng.standard_normal((M, D))
+    W = rng.standard_normal((D, V)) * 0.7
+    t = rng.integers(0, V, M)
+    loss, lse, dX, dW = ops.linear_ce(X, W, t, chunk=8, round_bf16=False)
+    tX = torch.from_numpy(X).requires_grad_(True)
+    tW = torch.from_numpy(W).requires_grad_(True)
+    tl = torch.nn.functional.cross_entropy(tX @ tW, torch.from_numpy(t))
+    tl.backward()
+    assert loss == pytest.approx(tl.item(), rel=1e-12)
+    np.testing.assert_allclose(dX, tX.grad.numpy(), rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(dW, tW.grad.numpy(), rtol=1e-10, atol=1e-14)
+    np.testing.assert_allclose(lse, torch.logsumexp(tX.detach() @ tW.detach(), -1).numpy(), rtol=1e-12)
+    for ch in (1, 7, 49, 50, 4096):
+        l2, lse2, dX2, dW2 = ops.linear_ce(X, W, t, chunk=ch, round_bf16=False)
+        assert l2 == pytest.approx(loss, rel=1e-12)
+        np.testing.assert_allclose(dX2, dX, rtol=1e-10, atol=1e-14)
+        np.testing.assert_allclose(dW2, dW, rtol=1e-10, atol=1e-14)
+    l0, lse0, dX0, dW0 = ops.linear_ce(X, np.zeros((D, V)), t, chunk=16)
+    assert l0 == pytest.approx(math.log(V), rel=1e-14)
+    np.testing.assert_allclose(dX0, 0.0, atol=0)
+    oh = np.zeros((M, V))
+    oh[np.arange(M), t] = 1.0
+    np.testing.assert_allclose(dW0, X.T @ ops.bf16_round((1.0 / V - oh) / M).astype(np.float64), rtol=1e-12)
+    # the rounded form equals the unfused composition CE(bf16(X @ W)) with bf16 dlogits
+    Xb, Wb = ops.bf16_round(X).astype(np.float64), ops.bf16_round(W).astype(np.float64)
+    lr, lser, dXr, dWr = ops.linear_ce(Xb, Wb, t, chunk=16)
+    cl, clse, cdl = ops.ce(ops.bf16_round(Xb @ Wb), t)
+    assert lr == pytest.approx(cl.mean(), rel=1e-12)
+    np.testing.assert_allclose(lser, clse, rtol=1e-12)
+    np.testing.assert_allclose(dWr, Xb.T @ ops.bf16_round(cdl).astype(np.float64), rtol=1e-10, atol=1e-14)
+
+
 def test_gelu_and_layernorm_pieces_vs_torch_float64():
     """The elementwise pieces of the model oracle against torch's own float64
     implementations (an independent code path): tanh-GELU and its derivative,

@@ -4,7 +4,9 @@ Both paths start from identical weights (same NumPy draws) and see identical
 batches; AdamW uses optax's warmup-cosine schedule. the
 loss curve matches within 1e-2 over 20 steps. The first step's parameter
 gradients are also compared (relative L2; the device path computes in bf16,
-the oracle in fp32 with bf16-rounded operands).
+the oracle in fp32 with bf16-rounded operands). Both loss paths of
+batch_loss are covered: the LM head then the CE, and the fused
+linear_cross_entropy.
 """
 import numpy as np
 import pytest
@@ -23,14 +25,15 @@ def _batches(n, vocab):
     return [rng.integers(0, vocab, (BS, SEQ + 1)).astype(np.int32) for _ in range(n)]
 
 
-def test_first_step_gradients_match_oracle(dev):
+@pytest.mark.parametrize("fused", [False, True], ids=["linear+ce", "linear_cross_entropy"])
+def test_first_step_gradients_match_oracle(dev, fused):
     import torch
     from nlearn_amd.model import init_model, tree_leaves
     from nlearn_amd.train import batch_loss
 
     params = init_model(0, device=dev)
     batch = _batches(1, 50257)[0]
-    loss = batch_loss(params, torch.from_numpy(batch).to(dev))
+    loss = batch_loss(params, torch.from_numpy(batch).to(dev), fused_lmhead=fused)
     loss.backward()
     ref_loss, ref_g = om.loss_and_grads(om.init_params(0), batch.astype(np.int64))
     assert abs(loss.item() - ref_loss) < 1e-2
@@ -43,8 +46,9 @@ def test_first_step_gradients_match_oracle(dev):
         assert err < 5e-2, (name, err)
 
 
-@pytest.mark.parametrize("graph", [False, True], ids=["eager", "hip_graph"])
-def test_loss_curve_matches_oracle_over_20_steps(dev, graph):
+@pytest.mark.parametrize("graph,fused", [(False, False), (True, False), (True, True)],
+                         ids=["eager", "hip_graph", "hip_graph-linear_cross_entropy"])
+def test_loss_curve_matches_oracle_over_20_steps(dev, graph, fused):
     import torch
     from nlearn_amd.model import init_model
     from nlearn_amd.train import AdamW, make_train_step, warmup_cosine_decay_schedule
@@ -54,7 +58,7 @@ def test_loss_curve_matches_oracle_over_20_steps(dev, graph):
     opt = AdamW(sched)
     params = init_model(0, device=dev)
     state = opt.init(params)
-    step = make_train_step(opt, graph=graph)
+    step = make_train_step(opt, graph=graph, fused_lmhead=fused)
     gpu = []
     for b in batches:
         params, state, loss = step(params, state, torch.from_numpy(b).to(dev))
