@@ -7,7 +7,10 @@
                                      fused HIP kernel; writes the bf16 weight shadows
 * ``make_train_step(optimizer)``     value_and_grad + update (train.py:328-341)
 * ``train(...)``                     offline loop on a synthetic uniform token stream
-                                     (train.py:482-622 streams a HF corpus instead)
+                                     (train.py:482-622 streams a HF corpus instead),
+                                     with the reference's checkpoint / resume files
+* ``save_checkpoint`` ... ``load_resume_state``  the checkpoint format (train.py:36-99;
+                                     nlearn_amd.checkpoint)
 
 ``python -m nlearn_amd.train --steps N`` runs offline: no dataset download, no
 tokenizer, no wandb (the reference needs all three, train.py:433-443,515-535).
@@ -23,12 +26,14 @@ import time
 import torch
 
 from . import _lib
+from .checkpoint import load_checkpoint, load_resume_state, save_checkpoint, save_resume_state  # noqa: F401
 from .kernels import wgrad
 from .kernels.cross_entropy import cross_entropy, linear_cross_entropy
 from .model import (BASELINE, ModelConfig, count_params, init_model, model_forward, model_forward_features,
                     output_projection, tree_leaves)
 
 WARMUP_STEPS = int(os.environ.get("NLEARN_WARMUP", "200"))
+CHECKPOINT_EVERY = int(os.environ.get("NLEARN_CHECKPOINT_EVERY", "1000"))
 PEAK_LR = 1e-3
 WEIGHT_DECAY = float(os.environ.get("NLEARN_WD", "0.1"))
 BATCH_SIZE = 32
@@ -329,27 +334,42 @@ class SyntheticTokens:
 
 
 def train(steps: int = 20, seq_len: int = 512, seed: int = 0, batch_size: int = BATCH_SIZE,
-          peak_lr: float = PEAK_LR, log_every: int = 10, cfg: ModelConfig | None = None) -> list:
-    """Offline training loop; returns the per-step losses."""
+          peak_lr: float = PEAK_LR, log_every: int = 10, cfg: ModelConfig | None = None, run_name=None,
+          resume: bool = False, checkpoint_every: int = CHECKPOINT_EVERY) -> list:
+    """Offline training loop; returns the per-step losses of the steps it ran.
+
+    As the reference's loop (train.py:537-605): every ``checkpoint_every``
+    steps it saves the parameters and the full resume state; ``resume=True``
+    continues from ``resume.pkl`` of ``run_name`` when one exists (parameters,
+    optimizer state incl. the schedule position, next step)."""
     cfg = cfg or ModelConfig(max_seq_len=max(seq_len, BASELINE.max_seq_len))
     warmup = min(WARMUP_STEPS, max(1, steps) // 5)
     sched = warmup_cosine_decay_schedule(0.0, peak_lr, warmup, max(1, steps), peak_lr / 10)
     opt = AdamW(sched)
-    params = init_model(seed, cfg)
+    start = 0
+    resumed = load_resume_state(opt, run_name) if resume else None
+    if resumed is not None:
+        params, state, start = resumed
+        print(f"Resumed from step {start} (resume.pkl)")
+    else:
+        params = init_model(seed, cfg)
+        state = opt.init(params)
     print(f"params: {count_params(params) / 1e6:.1f} M  bs={batch_size} seq={seq_len} warmup={warmup}")
-    state = opt.init(params)
     step_fn = make_train_step(opt, cfg)
-    data = SyntheticTokens(batch_size, seq_len, cfg.vocab_size, seed)
+    data = SyntheticTokens(batch_size, seq_len, cfg.vocab_size, seed + start)
     losses = []
     t0 = time.time()
-    for i in range(steps):
+    for step in range(start, steps):
         params, state, loss = step_fn(params, state, data.get_batch())
         losses.append(loss)
-        if (i + 1) % log_every == 0 or i + 1 == steps:
+        if (step + 1) % log_every == 0 or step + 1 == steps:
             torch.cuda.synchronize()
             dt = time.time() - t0
-            print(f"step {i + 1:5d}  loss {loss.item():.4f}  {(i + 1) * batch_size * seq_len / dt:,.0f} tok/s")
-    return [float(l) for l in torch.stack(losses).cpu()]
+            print(f"step {step + 1:5d}  loss {loss.item():.4f}  {(step + 1 - start) * batch_size * seq_len / dt:,.0f} tok/s")
+        if step > 0 and checkpoint_every > 0 and step % checkpoint_every == 0:
+            save_checkpoint(params, step, run_name=run_name)
+            save_resume_state(params, state, step + 1, run_name=run_name)
+    return [float(l) for l in torch.stack(losses).cpu()] if losses else []
 
 
 def main(argv=None):
@@ -359,8 +379,10 @@ def main(argv=None):
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--batch-size", type=int, default=BATCH_SIZE)
     ap.add_argument("--peak-lr", type=float, default=PEAK_LR)
+    ap.add_argument("--run-name", default=None)
+    ap.add_argument("--resume", action="store_true", help="continue from checkpoints/<run-name>/resume.pkl")
     a = ap.parse_args(argv)
-    train(a.steps, a.seq_len, a.seed, a.batch_size, a.peak_lr)
+    train(a.steps, a.seq_len, a.seed, a.batch_size, a.peak_lr, run_name=a.run_name, resume=a.resume)
 
 
 if __name__ == "__main__":

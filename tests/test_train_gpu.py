@@ -8,6 +8,8 @@ the oracle in fp32 with bf16-rounded operands). Both loss paths of
 batch_loss are covered: the LM head then the CE, and the fused
 linear_cross_entropy.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -70,3 +72,53 @@ def test_loss_curve_matches_oracle_over_20_steps(dev, graph, fused):
     print("cpu", np.round(cpu, 4).tolist())
     assert diff.max() < 1e-2, diff.tolist()
     assert np.isfinite(gpu).all()
+
+
+def test_resume_state_continues_the_step(dev, tmp_path, monkeypatch):
+    """save_resume_state after 3 steps, then a fresh optimizer and parameters
+    from load_resume_state continue exactly as the uninterrupted run
+    (train.py:76-99); save_checkpoint / load_checkpoint round-trip the
+    parameters bit for bit; train(resume=True) picks up at the saved step."""
+    import torch
+    from nlearn_amd.model import ModelConfig, init_model, tree_leaves
+    from nlearn_amd.train import (AdamW, load_checkpoint, load_resume_state, make_train_step, save_checkpoint,
+                                  save_resume_state, train, warmup_cosine_decay_schedule)
+
+    monkeypatch.chdir(tmp_path)
+    cfg = ModelConfig(max_seq_len=128)
+    rng = np.random.default_rng(31)
+    batches = [torch.from_numpy(rng.integers(0, 50257, (2, 129)).astype(np.int32)).to(dev) for _ in range(6)]
+    sched = warmup_cosine_decay_schedule(0.0, 1e-3, 2, 6, 1e-4)
+    opt = AdamW(sched)
+    params = init_model(0, cfg, dev)
+    state = opt.init(params)
+    step = make_train_step(opt, cfg)
+    for b in batches[:3]:
+        params, state, _ = step(params, state, b)
+    save_resume_state(params, state, 3, run_name="r")
+    path = save_checkpoint(params, 3, run_name="r")
+    back = load_checkpoint(path, device=dev)
+    for a, c in zip(tree_leaves(params), tree_leaves(back)):
+        assert torch.equal(a.detach(), c.detach())
+    la = []
+    for b in batches[3:]:
+        params, state, loss = step(params, state, b)
+        la.append(float(loss))
+    opt2 = AdamW(sched)
+    params2, state2, nxt = load_resume_state(opt2, run_name="r", device=dev)
+    assert nxt == 3 and state2["count"] == 3
+    step2 = make_train_step(opt2, cfg)
+    lb = []
+    for b in batches[3:]:
+        params2, state2, loss = step2(params2, state2, b)
+        lb.append(float(loss))
+    np.testing.assert_allclose(lb, la, rtol=1e-6, atol=1e-6)
+    for a, c in zip(tree_leaves(params), tree_leaves(params2)):
+        assert rel_l2(c.detach().cpu().numpy(), a.detach().cpu().numpy()) < 1e-5
+    # the loop itself: checkpoints every 2 steps, then a resumed run continues at step 3
+    small = ModelConfig(max_seq_len=64)
+    first = train(steps=4, seq_len=64, batch_size=2, log_every=100, cfg=small, run_name="t", checkpoint_every=2)
+    assert len(first) == 4 and os.path.exists("checkpoints/t/step_000002.pkl")
+    rest = train(steps=6, seq_len=64, batch_size=2, log_every=100, cfg=small, run_name="t", resume=True,
+                 checkpoint_every=2)
+    assert len(rest) == 3 and np.isfinite(rest).all()
