@@ -35,6 +35,8 @@ def _args():
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
+    ap.add_argument("--gemm-compare", action="store_true",
+                    help="time the BASELINE GEMM products here and through torch.matmul (hipBLASLt)")
     ap.add_argument("--fused-lmhead", action="store_true",
                     help="the loss through linear_cross_entropy (no logits kept between forward and backward)")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -274,10 +276,60 @@ def load_traffic(tag: str):
     return k.get("bytes_per_launch") if k else None
 
 
+def gemm_compare(reps: int = 20) -> None:
+    """The BASELINE GEMM products (configs[2]: M = 16384 and the model's (K, N),
+    each as forward NN, dX = dY.W^T (NT) and dW = X^T.dY (TN)) through this
+    library and through torch.matmul (hipBLASLt), both timed with HIP events
+    on the current stream after warm-up. One JSON line per product. torch's
+    dW comes out in bf16, ours in fp32 as the training step uses it."""
+    import torch
+
+    from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    M = 16384
+
+    def timeit(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    for K, N in ((512, 1536), (512, 512), (512, 2048), (2048, 512), (512, 50257)):
+        X = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
+        W = padded_empty(K, N, torch.bfloat16, dev)
+        W.copy_(torch.randn((K, N), generator=g, device=dev) * 0.05)
+        dY = padded_empty(M, N, torch.bfloat16, dev)
+        dY.copy_(torch.randn((M, N), generator=g, device=dev))
+        Y, dX = padded_empty(M, N, torch.bfloat16, dev), padded_empty(M, K, torch.bfloat16, dev)
+        dW = padded_empty(K, N, torch.float32, dev)
+        n = max(3, reps // 4) if N > 4096 else reps
+        for lay, ours, lib in (("NN", lambda: gemm_raw(X, W, out=Y), lambda: X @ W),
+                               ("NT", lambda: gemm_raw(dY, W, "N", "T", out=dX), lambda: dY @ W.t()),
+                               ("TN", lambda: gemm_raw(X, dY, "T", "N", out=dW), lambda: X.t() @ dY)):
+            mm, nn, kk = (M, N, K) if lay == "NN" else (M, K, N) if lay == "NT" else (K, N, M)
+            t_ours, t_lib = timeit(ours, n), timeit(lib, n)
+            fl = 2.0 * mm * nn * kk
+            print(json.dumps({"gemm": f"{lay}_{mm}x{nn}x{kk}", "ours_us": round(t_ours, 1),
+                              "hipblaslt_us": round(t_lib, 1), "ours_tflops": round(fl / t_ours / 1e6, 1),
+                              "hipblaslt_tflops": round(fl / t_lib / 1e6, 1),
+                              "speedup": round(t_lib / t_ours, 3)}), flush=True)
+
+
 def main():
     a = _args()
     if a.traffic_probe:
         traffic_probe()
+        return
+    if a.gemm_compare:
+        gemm_compare()
         return
     if a.traffic_summary:
         traffic_summary(*a.traffic_summary)
