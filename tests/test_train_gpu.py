@@ -48,6 +48,27 @@ def test_first_step_gradients_match_oracle(dev, fused):
         assert err < 5e-2, (name, err)
 
 
+def test_first_step_gradients_match_oracle_at_seq_4096(dev):
+    """BASELINE configs[4]'s long-sequence variant (seq 4096, 4096-row position
+    table): one sequence through the whole step, loss and every parameter
+    gradient against the NumPy oracle (flash at (8, 4096, 64) per layer)."""
+    import torch
+    from nlearn_amd.model import ModelConfig, init_model, tree_leaves
+    from nlearn_amd.train import batch_loss
+
+    cfg = ModelConfig(max_seq_len=4096)
+    params = init_model(0, cfg, dev)
+    batch = np.random.default_rng(4096).integers(0, 50257, (1, 4097)).astype(np.int32)
+    loss = batch_loss(params, torch.from_numpy(batch).to(dev), cfg)
+    loss.backward()
+    ocfg = om.Config(max_seq=4096)
+    ref_loss, ref_g = om.loss_and_grads(om.init_params(0, ocfg), batch.astype(np.int64), ocfg)
+    assert abs(loss.item() - ref_loss) < 1e-2
+    for i, (p, g) in enumerate(zip(tree_leaves(params), om._leaves(ref_g))):
+        err = rel_l2(p.grad.float().cpu().numpy(), g, floor=1e-8)
+        assert err < 5e-2, (i, err)
+
+
 @pytest.mark.parametrize("graph,fused", [(False, False), (True, False), (True, True)],
                          ids=["eager", "hip_graph", "hip_graph-linear_cross_entropy"])
 def test_loss_curve_matches_oracle_over_20_steps(dev, graph, fused):
