@@ -554,7 +554,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
 // dQ: workgroup = 128 queries, streams 64-key blocks up to the diagonal; the
 // K tile is read along rows (S) and down columns (dQ += dS K).
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(BwdArgs a) {
+__global__ __launch_bounds__(kThreads, 3) void flash_bwd_dq_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) uint16_t sK0[kBlk * kD];
   __shared__ __attribute__((aligned(16))) uint16_t sK1[kBlk * kD];
   __shared__ __attribute__((aligned(16))) uint16_t sV0[kBlk * kD];
