@@ -35,6 +35,8 @@ def _args():
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
+    ap.add_argument("--kernel-configs", action="store_true",
+                    help="time BASELINE configs[1] (flash) and configs[3] (CE) in isolation, beside torch's kernels")
     ap.add_argument("--gemm-compare", action="store_true",
                     help="time the BASELINE GEMM products here and through torch.matmul (hipBLASLt)")
     ap.add_argument("--fused-lmhead", action="store_true",
@@ -323,6 +325,68 @@ def gemm_compare(reps: int = 20) -> None:
                               "speedup": round(t_lib / t_ours, 3)}), flush=True)
 
 
+def kernel_configs(reps: int = 20) -> None:
+    """BASELINE configs[1] (causal flash forward and backward at (256, 512, 64)
+    and (32, 4096, 64), head dim 64, scale 1/8) and configs[3] (CE + dlogits at
+    (16384, 50257), logits ~ N(0, 2) bf16) in isolation: this library against
+    torch's own kernels for the same work (scaled_dot_product_attention with
+    is_causal, and cross_entropy forward + backward), HIP events on the current
+    stream after warm-up. One JSON line per case with the roofline fraction."""
+    import torch
+
+    from nlearn_amd.attention import flash_bwd_raw4, flash_fwd_raw4
+    from nlearn_amd.kernels.cross_entropy import ce_fwd_bwd_raw
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+
+    def timeit(fn, n=reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n * 1e3
+
+    for n, S in ((256, 512), (32, 4096)):
+        B, H = n // 8, 8
+        q, k, v, do = (torch.randn((B, H, S, 64), generator=g, device=dev).to(torch.bfloat16) for _ in range(4))
+        O, L = flash_fwd_raw4(q, k, v)
+        f = 2.0 * n * S * S * 64  # causal forward: QK^T and PV over the lower triangle
+        t_f = timeit(lambda: flash_fwd_raw4(q, k, v))
+        t_b = timeit(lambda: flash_bwd_raw4(q, k, v, O, do, L))
+        qr, kr, vr = (t.detach().clone().requires_grad_(True) for t in (q, k, v))
+        sdpa = torch.nn.functional.scaled_dot_product_attention
+        t_tf = timeit(lambda: sdpa(qr, kr, vr, is_causal=True))
+        out = sdpa(qr, kr, vr, is_causal=True)
+        t_tb = timeit(lambda: torch.autograd.grad(out, (qr, kr, vr), do, retain_graph=True))
+        for tag, t_o, t_t, w in (("fwd", t_f, t_tf, f), ("bwd", t_b, t_tb, 2.5 * f)):
+            print(json.dumps({"case": f"flash_{tag}_{n}x{S}x64", "ours_us": round(t_o, 1), "torch_us": round(t_t, 1),
+                              "ours_frac": round(w / t_o / 1e6 / PEAK_BF16_TFLOPS, 4),
+                              "torch_frac": round(w / t_t / 1e6 / PEAK_BF16_TFLOPS, 4),
+                              "speedup": round(t_t / t_o, 3)}), flush=True)
+    M, V = 16384, 50257
+    logits = (torch.randn((M, V), generator=g, device=dev) * 2.0).to(torch.bfloat16)
+    t = torch.randint(0, V, (M,), generator=g, device=dev)
+    t_o = timeit(lambda: ce_fwd_bwd_raw(logits, t), max(3, reps // 4))
+    lr = logits.detach().clone().requires_grad_(True)
+
+    def torch_ce():
+        loss = torch.nn.functional.cross_entropy(lr, t)
+        return torch.autograd.grad(loss, lr)
+
+    t_t = timeit(torch_ce, max(3, reps // 4))
+    byt = 4.0 * M * V + 12.0 * M
+    print(json.dumps({"case": f"ce_fwd_bwd_{M}x{V}", "ours_us": round(t_o, 1), "torch_us": round(t_t, 1),
+                      "ours_frac": round(byt / t_o / 1e3 / PEAK_HBM_GBS, 4),
+                      "torch_frac": round(byt / t_t / 1e3 / PEAK_HBM_GBS, 4), "speedup": round(t_t / t_o, 3)}),
+          flush=True)
+
+
 def main():
     a = _args()
     if a.traffic_probe:
@@ -330,6 +394,9 @@ def main():
         return
     if a.gemm_compare:
         gemm_compare()
+        return
+    if a.kernel_configs:
+        kernel_configs()
         return
     if a.traffic_summary:
         traffic_summary(*a.traffic_summary)
