@@ -35,6 +35,8 @@ def _args():
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
+    ap.add_argument("--torch-step", action="store_true",
+                    help="time the same training step written with plain PyTorch ops (a reference point)")
     ap.add_argument("--kernel-configs", action="store_true",
                     help="time BASELINE configs[1] (flash) and configs[3] (CE) in isolation, beside torch's kernels")
     ap.add_argument("--gemm-compare", action="store_true",
@@ -387,8 +389,73 @@ def kernel_configs(reps: int = 20) -> None:
           flush=True)
 
 
+def torch_step(bs: int, seq: int, steps: int, warmup: int) -> None:
+    """The same training step (BASELINE model, bs x seq tokens, AdamW) written
+    with plain PyTorch ops on the same GPU: bf16 weights and activations with
+    fp32 master weights in torch.optim.AdamW(fused=True), F.layer_norm, bf16
+    matmuls (hipBLASLt), scaled_dot_product_attention(is_causal=True), tanh
+    GELU, F.cross_entropy. Eager launches, timed like the main step. A
+    reference point for what the library buys over idiomatic PyTorch; prints
+    one JSON line."""
+    import torch
+    import torch.nn.functional as F
+
+    from nlearn_amd.model import ModelConfig, init_params_numpy, tree_leaves, tree_map
+
+    dev = torch.device("cuda:0")
+    cfg = ModelConfig(max_seq_len=max(512, seq))
+    params = tree_map(lambda a_: torch.from_numpy(a_).to(dev).requires_grad_(True), init_params_numpy(0, cfg))
+    opt = torch.optim.AdamW(tree_leaves(params), lr=1e-4, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.1,
+                            fused=True)
+    H, dh = cfg.n_heads, cfg.d_head
+    bf = torch.bfloat16
+
+    def loss_fn(batch):
+        ids, tgt = batch[:, :-1], batch[:, 1:]
+        e = params["embeddings"]
+        x = (e["token_embed"][ids] + e["pos_embed"][:seq]).to(bf)
+        for p in params["blocks"]:
+            h = F.layer_norm(x, (cfg.d_model,), p["ln1"]["gamma"].to(bf), p["ln1"]["beta"].to(bf), cfg.ln_eps)
+            qkv = (h @ p["attn"]["W_qkv"].to(bf)).view(bs, seq, 3, H, dh).permute(2, 0, 3, 1, 4)
+            a_ = F.scaled_dot_product_attention(qkv[0], qkv[1], qkv[2], is_causal=True)
+            x = x + a_.transpose(1, 2).reshape(bs, seq, cfg.d_model) @ p["attn"]["W_o"].to(bf)
+            h = F.layer_norm(x, (cfg.d_model,), p["ln2"]["gamma"].to(bf), p["ln2"]["beta"].to(bf), cfg.ln_eps)
+            f = p["ffn"]
+            u = F.gelu(h @ f["W1"].to(bf) + f["b1"].to(bf), approximate="tanh")
+            x = x + u @ f["W2"].to(bf) + f["b2"].to(bf)
+        lf = params["ln_final"]
+        x = F.layer_norm(x, (cfg.d_model,), lf["gamma"].to(bf), lf["beta"].to(bf), cfg.ln_eps)
+        logits = x @ params["lm_head"].to(bf)
+        return F.cross_entropy(logits.view(-1, cfg.vocab_size).float(), tgt.reshape(-1).long())
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    batches = [torch.randint(0, cfg.vocab_size, (bs, seq + 1), generator=g, device=dev) for _ in range(4)]
+
+    def step(b):
+        opt.zero_grad(set_to_none=True)
+        loss = loss_fn(b)
+        loss.backward()
+        opt.step()
+        return loss
+
+    for i in range(warmup):
+        step(batches[i % 4])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        loss = step(batches[i % 4])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    print(json.dumps({"torch_step": f"d512/8h/4L vocab50257 bs{bs} seq{seq}", "ms_per_step": round(dt / steps * 1e3, 3),
+                      "tokens_per_s": round(bs * seq * steps / dt, 1), "final_loss": round(float(loss.detach()), 4),
+                      "peak_hbm_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2)}), flush=True)
+
+
 def main():
     a = _args()
+    if a.torch_step:
+        torch_step(a.batch_size, a.seq_len, a.steps, a.warmup)
+        return
     if a.traffic_probe:
         traffic_probe()
         return
@@ -494,7 +561,7 @@ def main():
             "six_n_t_tflops": round(fl["six_n_t"] / (dt / a.steps) / 1e12, 2),
             "peak_hbm_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
             "nlearn_kernels_busy_ratio": round(probed_ms / ms, 4),
-            "final_loss": round(float(loss), 4),
+            "final_loss": round(float(loss.detach()), 4),
             "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                         for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["time_per_step_ms"])},
         },
