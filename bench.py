@@ -470,7 +470,7 @@ def main():
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the data-parallel step would all-reduce "
-              "gradients over RCCL; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "the gradients over RCCL before AdamW). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
