@@ -387,6 +387,16 @@ def kernel_configs(reps: int = 20) -> None:
                       "ours_frac": round(byt / t_o / 1e3 / PEAK_HBM_GBS, 4),
                       "torch_frac": round(byt / t_t / 1e3 / PEAK_HBM_GBS, 4), "speedup": round(t_t / t_o, 3)}),
           flush=True)
+    # what the box sustains for plain traffic: a 2 GiB device copy (read + write), fill (write), sum (read)
+    del logits, lr
+    n = 2 * 2**30 // 4
+    src = torch.randn(n, generator=g, device=dev)
+    dst = torch.empty_like(src)
+    for tag, fn, byt in (("hbm_copy_2GiB", lambda: dst.copy_(src), 8.0 * n), ("hbm_fill_2GiB", lambda: dst.fill_(1.0), 4.0 * n),
+                         ("hbm_sum_2GiB", lambda: src.sum(), 4.0 * n)):
+        t_x = timeit(fn, 10)
+        print(json.dumps({"case": tag, "torch_us": round(t_x, 1), "tbs": round(byt / t_x / 1e6, 3),
+                          "torch_frac": round(byt / t_x / 1e3 / PEAK_HBM_GBS, 4)}), flush=True)
 
 
 def torch_step(bs: int, seq: int, steps: int, warmup: int) -> None:
