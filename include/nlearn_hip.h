@@ -360,7 +360,8 @@ int nl_embedding_fwd(void* stream, int batch, int seq, int D, int vocab, const i
                      const float* tok, const float* pos, nl_bf16* out);
 
 /* dtok[ids[t]] += dx[t] (fp32 atomics: the caller zeroes dtok; repeated ids are
- * summed in hardware order), dpos[s] (+)= sum_b dx[b][s] in batch order.
+ * summed in hardware order), dpos[s] (+)= sum_b dx[b][s] in batch order for
+ * s < seq (rows of dpos at or past seq are not touched). One kernel launch.
  * The autodiff of the gather in model.py:75-85. */
 int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
                      const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos);

@@ -335,29 +335,30 @@ __global__ __launch_bounds__(128) void embed_fwd_kernel(int S, int D, const int3
   }
 }
 
-// dtok[ids[t]] += dx[t] with fp32 atomics (rows of repeated tokens are summed in
-// hardware order, the one non-deterministic sum of the step); ids outside
-// [0, vocab) contribute nothing.
-__global__ __launch_bounds__(128) void embed_bwd_tok_kernel(int D, const int32_t* __restrict__ ids,
-                                                            const uint16_t* __restrict__ dx, float* __restrict__ dtok,
-                                                            int vocab) {
-  const int t = blockIdx.x;
+// One launch for both tables. Workgroups [0, S) form dpos[s] (+)= sum_b dx[b, s]
+// in batch order (launched first: each reads B rows); workgroups [S, S + B*S)
+// add dx[t] into dtok[ids[t]] with fp32 atomics (rows of repeated tokens are
+// summed in hardware order, the one non-deterministic sum of the step); ids
+// outside [0, vocab) contribute nothing.
+__global__ __launch_bounds__(128) void embed_bwd_kernel(int B, int S, int D, const int32_t* __restrict__ ids,
+                                                        const uint16_t* __restrict__ dx, float* __restrict__ dtok,
+                                                        int vocab, float* __restrict__ dpos, int accumulate) {
+  if ((int)blockIdx.x < S) {
+    const int s = blockIdx.x;
+    for (int c = threadIdx.x; c < D; c += 128) {
+      float a = 0.f;
+#pragma unroll 8
+      for (int b = 0; b < B; ++b) a += bf16_to_f32(dx[((int64_t)b * S + s) * D + c]);
+      float* o = dpos + (int64_t)s * D + c;
+      *o = accumulate ? *o + a : a;
+    }
+    return;
+  }
+  const int t = blockIdx.x - S;
   const int id = ids[t];
   if (id < 0 || id >= vocab) return;
   for (int c = threadIdx.x; c < D; c += 128)
     atomicAdd(dtok + (int64_t)id * D + c, bf16_to_f32(dx[(int64_t)t * D + c]));
-}
-
-// dpos[s] (+)= sum_b dx[b, s] in batch order.
-__global__ __launch_bounds__(128) void embed_bwd_pos_kernel(int B, int S, int D, const uint16_t* __restrict__ dx,
-                                                            float* __restrict__ dpos, int accumulate) {
-  const int s = blockIdx.x;
-  for (int c = threadIdx.x; c < D; c += 128) {
-    float a = 0.f;
-    for (int b = 0; b < B; ++b) a += bf16_to_f32(dx[((int64_t)b * S + s) * D + c]);
-    float* o = dpos + (int64_t)s * D + c;
-    *o = accumulate ? *o + a : a;
-  }
 }
 
 int vectors_per_lane(int D) {
@@ -481,9 +482,8 @@ extern "C" int nl_embedding_bwd(void* stream, int batch, int seq, int D, int voc
   if (batch < 0 || seq < 0 || D <= 0 || vocab <= 0) return nl_set_error(NL_EINVAL, "embedding_bwd: bad shape");
   if (batch == 0 || seq == 0) return NL_OK;
   if (!ids || !dx || !dtok || !dpos) return nl_set_error(NL_EINVAL, "embedding_bwd: null pointer");
-  if ((int64_t)batch * seq > 0x7fffffff) return nl_set_error(NL_EINVAL, "embedding_bwd: too many tokens");
-  hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(embed_bwd_tok_kernel, dim3(batch * seq), dim3(128), 0, st, D, ids, dx, dtok, vocab);
-  hipLaunchKernelGGL(embed_bwd_pos_kernel, dim3(seq), dim3(128), 0, st, batch, seq, D, dx, dpos, accumulate_pos);
+  if ((int64_t)batch * seq + seq > 0x7fffffff) return nl_set_error(NL_EINVAL, "embedding_bwd: too many tokens");
+  hipLaunchKernelGGL(embed_bwd_kernel, dim3(seq + batch * seq), dim3(128), 0, (hipStream_t)stream, batch, seq, D, ids,
+                     dx, dtok, vocab, dpos, accumulate_pos);
   return nl_check_launch("nl_embedding_bwd");
 }

@@ -8,7 +8,8 @@
   tanh-GELU and biases) as two GEMMs whose epilogues add the biases and apply
   the GELU; the backward's dX GEMM applies the GELU derivative in its
   epilogue, so no elementwise kernel runs between the GEMMs.
-* ``embedding(ids, tok, pos)``: token + learned-position lookup (model.py:75-85).
+* ``embedding(ids, tok, pos)``: token + learned-position lookup (model.py:75-85);
+  ``embedding_layer_norm`` is the lookup together with the first LayerNorm.
 
 Every op is an autograd Function whose forward and backward are C-ABI calls;
 there is no framework fallback.
@@ -224,38 +225,91 @@ def ffn(x: torch.Tensor, W1: torch.Tensor, b1: torch.Tensor, W2: torch.Tensor, b
 # ---------------------------------------------------------------------------
 
 
+def _embedding_fwd(ids, tok, pos):
+    """-> (bf16 (B, S, D) lookup, int32 ids, dims for the backward)."""
+    B, S = ids.shape
+    V, D = tok.shape
+    if S > pos.shape[0]:
+        raise ValueError(f"embedding: sequence {S} exceeds the position table ({pos.shape[0]})")
+    ids32 = ids.to(torch.int32).contiguous()
+    t, p = _param(tok), _param(pos)
+    _check_device(ids32, t, p)
+    out = torch.empty((B, S, D), dtype=_BF16, device=ids.device)
+    _lib.call("nl_embedding_fwd", _stream(out), B, S, D, V, ids32.data_ptr(), t.data_ptr(), p.data_ptr(),
+              out.data_ptr())
+    return out, ids32, (B, S, D, V, tuple(pos.shape))
+
+
 class _Embedding(torch.autograd.Function):
     @staticmethod
     def forward(ctx, ids, tok, pos):
-        B, S = ids.shape
-        V, D = tok.shape
-        if S > pos.shape[0]:
-            raise ValueError(f"embedding: sequence {S} exceeds the position table ({pos.shape[0]})")
-        ids32 = ids.to(torch.int32).contiguous()
-        t, p = _param(tok), _param(pos)
-        _check_device(ids32, t, p)
-        out = torch.empty((B, S, D), dtype=_BF16, device=ids.device)
-        _lib.call("nl_embedding_fwd", _stream(out), B, S, D, V, ids32.data_ptr(), t.data_ptr(), p.data_ptr(),
-                  out.data_ptr())
+        out, ids32, ctx.dims = _embedding_fwd(ids, tok, pos)
         ctx.save_for_backward(ids32)
-        ctx.dims = (B, S, D, V, tuple(pos.shape))
         ctx.bufs = (grad_buffer(tok), grad_buffer(pos))
         return out
 
     @staticmethod
     def backward(ctx, dx):
         (ids32,) = ctx.saved_tensors
-        B, S, D, V, pshape = ctx.dims
-        dx = dx.to(_BF16).contiguous()
-        gt, gp = ctx.bufs
-        # zero_() is a fill kernel (no memset node when the step is captured)
-        dtok = gt.zero_() if gt is not None else torch.zeros((V, D), dtype=_F32, device=dx.device)
-        dpos = gp.zero_() if gp is not None else torch.zeros(pshape, dtype=_F32, device=dx.device)
-        _lib.call("nl_embedding_bwd", _stream(dx), B, S, D, V, ids32.data_ptr(), dx.data_ptr(), dtok.data_ptr(),
-                  dpos.data_ptr(), 0)
-        return None, *_unless_buffered(ctx.bufs, (dtok, dpos))
+        return None, *_embedding_bwd(ids32, dx, ctx.dims, ctx.bufs)
+
+
+def _embedding_bwd(ids32, dx, dims, bufs):
+    """(dtok, dpos) of the lookup, None where a main_grad buffer took them."""
+    B, S, D, V, pshape = dims
+    dx = dx.to(_BF16).contiguous()
+    gt, gp = bufs
+    # zero_() is a fill kernel (no memset node when the step is captured); the
+    # kernel writes rows [0, S) of dpos, so only longer tables need one
+    dtok = gt.zero_() if gt is not None else torch.zeros((V, D), dtype=_F32, device=dx.device)
+    if gp is None:
+        dpos = torch.zeros(pshape, dtype=_F32, device=dx.device)
+    else:
+        dpos = gp.zero_() if pshape[0] > S else gp
+    _lib.call("nl_embedding_bwd", _stream(dx), B, S, D, V, ids32.data_ptr(), dx.data_ptr(), dtok.data_ptr(),
+              dpos.data_ptr(), 0)
+    return _unless_buffered(bufs, (dtok, dpos))
 
 
 def embedding(ids: torch.Tensor, tok: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
     """bf16 (B, S, D) = tok[ids] + pos[:S] for int ids (B, S)."""
     return _Embedding.apply(ids, tok, pos)
+
+
+class _EmbeddingLayerNorm(torch.autograd.Function):
+    """The lookup and the first block's LayerNorm as one node: the residual
+    stream x and LN(x) both leave it, so in the backward the LayerNorm kernel
+    adds x's other gradient (dres) while forming its own, and the lookup's
+    backward reads the sum (no separate add of the two gradients)."""
+
+    @staticmethod
+    def forward(ctx, ids, tok, pos, gamma, beta, eps):
+        ctx.set_materialize_grads(False)
+        x, ids32, ctx.dims = _embedding_fwd(ids, tok, pos)
+        x2 = x.view(-1, x.shape[-1])
+        g, b = _param(gamma), _param(beta)
+        y, _, mean, rstd = layer_norm_fwd_raw(x2, g, b, eps)
+        ctx.save_for_backward(ids32, x2, mean, rstd, g)
+        ctx.bufs = (grad_buffer(tok), grad_buffer(pos))
+        ctx.ln_bufs = (grad_buffer(gamma), grad_buffer(beta))
+        return y.view(x.shape), x2.view(x.shape)
+
+    @staticmethod
+    def backward(ctx, dy, dx):
+        ids32, x2, mean, rstd, g = ctx.saved_tensors
+        ln_grads = (None, None)
+        if dy is not None:
+            dx2, dg, db = layer_norm_bwd_raw(_rows(dy), x2, mean, rstd, g, _rows(dx) if dx is not None else None,
+                                             *ctx.ln_bufs)
+            dx = dx2
+            ln_grads = _unless_buffered(ctx.ln_bufs, (dg, db))
+        if dx is None:
+            return None, None, None, *ln_grads, None
+        return None, *_embedding_bwd(ids32, dx, ctx.dims, ctx.bufs), *ln_grads, None
+
+
+def embedding_layer_norm(ids: torch.Tensor, tok: torch.Tensor, pos: torch.Tensor, gamma: torch.Tensor,
+                         beta: torch.Tensor, eps: float = 1e-5):
+    """(LN(x), x) with x = embedding(ids, tok, pos): the lookup and the first
+    LayerNorm, whose backward also takes in x's residual-stream gradient."""
+    return _EmbeddingLayerNorm.apply(ids, tok, pos, gamma, beta, eps)

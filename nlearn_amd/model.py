@@ -168,12 +168,13 @@ def block_forward(p, x: torch.Tensor, cfg: ModelConfig) -> torch.Tensor:
     return x + r
 
 
-def _block(p, x: torch.Tensor, r, cfg: ModelConfig):
+def _block(p, x: torch.Tensor, r, cfg: ModelConfig, h=None):
     """Block with its residual adds deferred: the stream arrives as x + r (r may
-    be None) and leaves as (x', r'); each add is folded into the next LayerNorm."""
-    if r is None:
+    be None) and leaves as (x', r'); each add is folded into the next LayerNorm.
+    ``h`` is LN1(x) when the caller already formed it."""
+    if h is None and r is None:
         h = layer_norm(p["ln1"], x, cfg.ln_eps)
-    else:
+    elif h is None:
         h, x = fused.add_layer_norm(x, r, p["ln1"]["gamma"], p["ln1"]["beta"], cfg.ln_eps)
     a = attention_forward(p["attn"], h, cfg)
     h2, x = fused.add_layer_norm(x, a, p["ln2"]["gamma"], p["ln2"]["beta"], cfg.ln_eps)
@@ -181,10 +182,18 @@ def _block(p, x: torch.Tensor, r, cfg: ModelConfig):
 
 
 def model_forward_features(params, token_ids: torch.Tensor, cfg: ModelConfig = BASELINE) -> torch.Tensor:
-    """Hidden states after the final LayerNorm, bf16 (bs, seq, d)."""
-    x = embed(params, token_ids)
+    """Hidden states after the final LayerNorm, bf16 (bs, seq, d). The lookup
+    and the first block's LN1 are one node (fused.embedding_layer_norm)."""
+    blocks = params["blocks"]
     r = None
-    for bp in params["blocks"]:
+    if blocks:
+        e, ln1 = params["embeddings"], blocks[0]["ln1"]
+        h, x = fused.embedding_layer_norm(token_ids, e["token_embed"], e["pos_embed"], ln1["gamma"], ln1["beta"],
+                                          cfg.ln_eps)
+        x, r = _block(blocks[0], x, None, cfg, h=h)
+    else:
+        x = embed(params, token_ids)
+    for bp in blocks[1:]:
         x, r = _block(bp, x, r, cfg)
     lf = params["ln_final"]
     if r is None:

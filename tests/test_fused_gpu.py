@@ -270,3 +270,39 @@ def test_embedding_invalid_ids_give_nan_rows(dev):
     out = embedding(ids, tok, pos).float().cpu()
     assert torch.isnan(out[0, 1]).all() and torch.isnan(out[0, 2]).all()
     assert (out[0, 0] == 1).all() and (out[0, 3] == 1).all()
+
+
+@pytest.mark.parametrize("B,S,P", [(2, 64, 64), (3, 37, 40)])
+def test_embedding_layer_norm_matches_the_composition(dev, B, S, P):
+    """embedding_layer_norm == layer_norm(embedding(.)) with both outputs' gradients, its
+    parameter gradients written into main_grad buffers that start as NaN (every element
+    must be overwritten; the position table past S must come back zero)."""
+    import torch
+    from nlearn_amd.kernels.fused import embedding, embedding_layer_norm, layer_norm
+
+    V, D = 1000, 64
+    rng = np.random.default_rng(B + S + P)
+    ids = torch.from_numpy(rng.integers(0, V, (B, S)).astype(np.int32)).to(dev)
+    tables = [rng.standard_normal((V, D)) * 0.5, rng.standard_normal((P, D)) * 0.5,
+              1 + 0.1 * rng.standard_normal(D), 0.1 * rng.standard_normal(D)]
+    dy = _dev_bf16(rng.standard_normal((B, S, D)), dev)
+    dx = _dev_bf16(rng.standard_normal((B, S, D)), dev)
+    ref = [_f32(a, dev).requires_grad_(True) for a in tables]
+    x = embedding(ids, ref[0], ref[1])
+    h = layer_norm(x, ref[2], ref[3])
+    torch.autograd.backward([h, x], [dy, dx])
+    fused = [_f32(a, dev).requires_grad_(True) for a in tables]
+    for t in fused:
+        t.main_grad = torch.full_like(t, float("nan"))
+    h1, x1 = embedding_layer_norm(ids, *fused)
+    torch.autograd.backward([h1, x1], [dy, dx])
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h) and torch.equal(x1, x)
+    for got, want in zip(fused, ref):
+        assert got.grad is None
+        g = _np(got.main_grad)
+        assert np.isfinite(g).all()
+        # the fused backward adds x's gradient in fp32 before one bf16 rounding,
+        # the composition rounds the LayerNorm's dx to bf16 first
+        assert rel_l2(g, _np(want.grad)) <= 1e-2
+    assert not _np(fused[1].main_grad)[S:].any()
