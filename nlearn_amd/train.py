@@ -58,8 +58,9 @@ def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_l
     linear_cross_entropy path instead (train.py:279-283), which keeps no logits
     between the forward and the backward and recomputes them in the backward.
     """
-    input_ids = batch[:, :-1]
-    target_ids = batch[:, 1:]
+    # both shifted views in one contiguous copy (one kernel; the lookup and the
+    # CE then read them in place)
+    input_ids, target_ids = torch.stack((batch[:, :-1], batch[:, 1:])).unbind(0)
     if FUSED_LMHEAD if fused_lmhead is None else fused_lmhead:
         x = model_forward_features(params, input_ids, cfg)
         return linear_cross_entropy(x.reshape(-1, cfg.d_model), output_projection(params), target_ids.reshape(-1))
@@ -282,6 +283,7 @@ class _GraphedStep:
         self.graph = None
         self.static_batch = None
         self.static_loss = None
+        self.seed = None
 
     def _capture(self, params, state, batch):
         leaves = tree_leaves(params)
@@ -291,12 +293,15 @@ class _GraphedStep:
         for p in leaves:
             p.grad = None
         wgrad.prepare(batch.device)  # create the side stream outside the capture
+        # the backward's seed d(loss)/d(loss) = 1, made once and kept (every
+        # replay reads it): backward() without it records a fill kernel
+        self.seed = seed = torch.ones((), dtype=torch.float32, device=batch.device)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             loss = batch_loss(params, self.static_batch, self.cfg, self.fused_lmhead)
             with self.overlap(loss.device):
-                loss.backward()
+                loss.backward(seed)
             with torch.no_grad():
                 self.opt.apply(params, state)
         self.static_loss = loss.detach()
