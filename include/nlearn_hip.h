@@ -346,6 +346,24 @@ int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy, const nl_
                      const float* mean, const float* rstd, const float* gamma, const nl_bf16* dres,
                      nl_bf16* dx, float* dgamma, float* dbeta, int accumulate, void* ws, size_t ws_bytes);
 
+/* nl_layernorm_bwd with the parameter sums deferred, for a chain of LayerNorm
+ * backwards whose dgamma / dbeta only an optimizer reads later (the model's 9
+ * per step): dx is formed as above, but this call's sums stay as partial rows
+ * in ws (keep it until they are reduced), and the same launch reduces the
+ * partials that an earlier deferred call left in prev_ws (prev_rows x prev_D;
+ * prev_ws NULL: nothing to reduce) into prev_dgamma / prev_dbeta (+= if
+ * prev_accumulate). One kernel launch instead of two per LayerNorm; the sums
+ * are those of nl_layernorm_bwd, bit for bit. */
+int nl_layernorm_bwd_deferred(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x,
+                              const float* mean, const float* rstd, const float* gamma, const nl_bf16* dres,
+                              nl_bf16* dx, void* ws, size_t ws_bytes, int prev_rows, int prev_D,
+                              const void* prev_ws, float* prev_dgamma, float* prev_dbeta, int prev_accumulate);
+
+/* Reduces the partial rows a deferred call left in ws (rows, D as in that call)
+ * into dgamma / dbeta (+= if accumulate): the last link of such a chain. */
+int nl_layernorm_param_sums(void* stream, int rows, int D, const void* ws, float* dgamma, float* dbeta,
+                            int accumulate);
+
 /* out[c] (+)= sum_r x[r][c] over a bf16 [rows][ld] matrix: the bias gradients
  * db = sum_rows dY of the FFN biases (autodiff of model.py:266-277 with the
  * benchmark's b1, b2). Fixed summation order; workspace nl_colsum_ws_bytes(). */

@@ -75,6 +75,9 @@ _SIGNATURES = {
     "nl_layernorm_fwd": [_P, _I, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P],
     "nl_layernorm_bwd_ws_bytes": [_I, _I],
     "nl_layernorm_bwd": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t],
+    "nl_layernorm_bwd_deferred": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I, _I, _P, _P, _P,
+                                  _I],
+    "nl_layernorm_param_sums": [_P, _I, _I, _P, _P, _P, _I],
     "nl_colsum_ws_bytes": [_I, _I],
     "nl_colsum_bf16": [_P, _I, _I, _P, _I64, _P, _I, _P, ctypes.c_size_t],
     "nl_embedding_fwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P],

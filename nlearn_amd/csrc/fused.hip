@@ -127,13 +127,83 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, in
   }
 }
 
-// dx = dLN(dy) (+ dres). Each workgroup also writes one partial row of dgamma
-// and one of dbeta (its 4 waves combined in wave order).
+// out[c] (+)= sum_{p<P} part[p][c] for one or two (part, out) pairs
+// (blockIdx.y picks the pair), summed in a fixed order. A workgroup owns 16
+// columns: thread (ph, q), ph < 64, q < 4, sums rows p = ph, ph+64, ... of
+// columns [4q, 4q+4) of its strip; the 64 phase sums are then added in groups
+// of 4 (phases 4g..4g+3) and the 16 group sums in g order. The strips are
+// narrow so that a 512-column sum still spreads over 32 workgroups per pair
+// with every row load in flight at once (P <= 1024: 16 loads a thread).
+__device__ __forceinline__ void sum_partials_strip(int bx, int pair, int P, int D, const float* __restrict__ part0,
+                                                   float* __restrict__ out0, const float* __restrict__ part1,
+                                                   float* __restrict__ out1, int accumulate) {
+  __shared__ float s[64][17];
+  __shared__ float s2[16][17];
+  const float* __restrict__ part = pair ? part1 : part0;
+  float* __restrict__ out = pair ? out1 : out0;
+  const int q = threadIdx.x & 3, ph = threadIdx.x >> 2;
+  const int c = bx * 16 + q * 4;
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  if ((D & 3) == 0) {
+    if (c < D) {
+#pragma unroll 16
+      for (int p = ph; p < P; p += 64) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)p * D + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[j] += v[j];
+      }
+    }
+  } else {
+#pragma unroll 4
+    for (int p = ph; p < P; p += 64) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c + j < D) a[j] += part[(int64_t)p * D + c + j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s[ph][q * 4 + j] = a[j];
+  __syncthreads();
+  {
+    const int col = threadIdx.x & 15, g = threadIdx.x >> 4;
+    s2[g][col] = ((s[4 * g][col] + s[4 * g + 1][col]) + s[4 * g + 2][col]) + s[4 * g + 3][col];
+  }
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int cc = bx * 16 + threadIdx.x;
+    if (cc < D) {
+      float t = 0.f;
+#pragma unroll
+      for (int g = 0; g < 16; ++g) t += s2[g][threadIdx.x];
+      out[cc] = accumulate ? out[cc] + t : t;
+    }
+  }
+}
+
+// A reduction of partial rows that rides along in another kernel's launch.
+struct PartialSums {
+  int P, D, strips;  // strips: (D + 15) / 16 workgroups per pair; 0 = none
+  const float* part_g;
+  float* dgamma;
+  const float* part_b;
+  float* dbeta;
+  int accumulate;
+};
+
+// dx = dLN(dy) (+ dres). Each of the first nblk workgroups also writes one
+// partial row of dgamma and one of dbeta (its 4 waves combined in wave order).
+// Workgroups past nblk reduce `prev`, the partial rows of an earlier call.
 template <int VPL>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
     int rows, int D, const uint16_t* __restrict__ dy, const uint16_t* __restrict__ x, const float* __restrict__ mean_in,
     const float* __restrict__ rstd_in, const float* __restrict__ gamma, const uint16_t* __restrict__ dres,
-    uint16_t* __restrict__ dx, float* __restrict__ part_g, float* __restrict__ part_b) {
+    uint16_t* __restrict__ dx, float* __restrict__ part_g, float* __restrict__ part_b, int nblk, PartialSums prev) {
+  if ((int)blockIdx.x >= nblk) {
+    const int j = blockIdx.x - nblk;
+    sum_partials_strip(j % prev.strips, j / prev.strips, prev.P, prev.D, prev.part_g, prev.dgamma, prev.part_b,
+                       prev.dbeta, prev.accumulate);
+    return;
+  }
   __shared__ float sg[VPL * 512];
   __shared__ float sb[VPL * 512];
   const int lane = threadIdx.x & 63;
@@ -148,7 +218,7 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
   }
   // Rows are software-pipelined: the next row's dy, x, dres, mean and rstd are
   // in flight while this row is computed and stored.
-  const int stride = gridDim.x * kRowsPerBlock;
+  const int stride = nblk * kRowsPerBlock;
   int row = blockIdx.x * kRowsPerBlock + wave;
   u32x4 dv[VPL], xv[VPL], rv[VPL];
   float mu = 0.f, rs = 0.f;
@@ -231,57 +301,10 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_bwd_kernel(
   }
 }
 
-// out[c] (+)= sum_{p<P} part[p][c] for one or two (part, out) pairs
-// (blockIdx.y picks the pair), summed in a fixed order. A workgroup owns 16
-// columns: thread (ph, q), ph < 64, q < 4, sums rows p = ph, ph+64, ... of
-// columns [4q, 4q+4) of its strip; the 64 phase sums are then added in groups
-// of 4 (phases 4g..4g+3) and the 16 group sums in g order. The strips are
-// narrow so that a 512-column sum still spreads over 32 workgroups per pair
-// with every row load in flight at once (P <= 1024: 16 loads a thread).
 __global__ __launch_bounds__(256) void sum_partials_kernel(int P, int D, const float* __restrict__ part0,
                                                            float* __restrict__ out0, const float* __restrict__ part1,
                                                            float* __restrict__ out1, int accumulate) {
-  __shared__ float s[64][17];
-  __shared__ float s2[16][17];
-  const float* __restrict__ part = blockIdx.y ? part1 : part0;
-  float* __restrict__ out = blockIdx.y ? out1 : out0;
-  const int q = threadIdx.x & 3, ph = threadIdx.x >> 2;
-  const int c = blockIdx.x * 16 + q * 4;
-  float a[4] = {0.f, 0.f, 0.f, 0.f};
-  if ((D & 3) == 0) {
-    if (c < D) {
-#pragma unroll 16
-      for (int p = ph; p < P; p += 64) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)p * D + c);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[j] += v[j];
-      }
-    }
-  } else {
-#pragma unroll 4
-    for (int p = ph; p < P; p += 64) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        if (c + j < D) a[j] += part[(int64_t)p * D + c + j];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) s[ph][q * 4 + j] = a[j];
-  __syncthreads();
-  {
-    const int col = threadIdx.x & 15, g = threadIdx.x >> 4;
-    s2[g][col] = ((s[4 * g][col] + s[4 * g + 1][col]) + s[4 * g + 2][col]) + s[4 * g + 3][col];
-  }
-  __syncthreads();
-  if (threadIdx.x < 16) {
-    const int cc = blockIdx.x * 16 + threadIdx.x;
-    if (cc < D) {
-      float t = 0.f;
-#pragma unroll
-      for (int g = 0; g < 16; ++g) t += s2[g][threadIdx.x];
-      out[cc] = accumulate ? out[cc] + t : t;
-    }
-  }
+  sum_partials_strip(blockIdx.x, blockIdx.y, P, D, part0, out0, part1, out1, accumulate);
 }
 
 // Partial column sums of a bf16 [rows][cols] matrix (row stride ld, ld % 8 == 0):
@@ -406,27 +429,45 @@ extern "C" size_t nl_layernorm_bwd_ws_bytes(int rows, int D) {
   return (size_t)2 * ln_bwd_blocks(rows) * D * sizeof(float);
 }
 
-extern "C" int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x, const float* mean,
-                                const float* rstd, const float* gamma, const nl_bf16* dres, nl_bf16* dx, float* dgamma,
-                                float* dbeta, int accumulate, void* ws, size_t ws_bytes) {
+#define NL_TRY(x)        \
+  do {                   \
+    int rc_ = (x);       \
+    if (rc_) return rc_; \
+  } while (0)
+
+namespace nl {
+namespace {
+PartialSums no_partial_sums() {
+  PartialSums r{};
+  return r;
+}
+
+// Checks the arguments of one LayerNorm backward and launches ln_bwd_kernel,
+// its parameter sums left as partial rows in ws, plus the workgroups of prev.
+int ln_bwd_launch(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x, const float* mean,
+                  const float* rstd, const float* gamma, const nl_bf16* dres, nl_bf16* dx, void* ws, size_t ws_bytes,
+                  const PartialSums& prev, const char* who) {
   if (rows < 0 || D <= 0 || (D % 8) != 0 || D > kMaxD)
-    return nl_set_error(NL_EINVAL, "layernorm: need 0 < D <= 4096 and D % 8 == 0");
-  if (rows == 0) return NL_OK;
-  if (!dy || !x || !mean || !rstd || !gamma || !dx || !dgamma || !dbeta || !ws)
-    return nl_set_error(NL_EINVAL, "layernorm_bwd: null pointer");
-  if ((((uintptr_t)dy | (uintptr_t)x | (uintptr_t)dx | (uintptr_t)dres | (uintptr_t)gamma | (uintptr_t)ws) & 15) != 0)
-    return nl_set_error(NL_EALIGN, "layernorm_bwd: buffers must be 16-byte aligned");
-  if (ws_bytes < nl_layernorm_bwd_ws_bytes(rows, D))
-    return nl_set_error(NL_EINVAL, "layernorm_bwd: workspace smaller than nl_layernorm_bwd_ws_bytes()");
-  const int blocks = ln_bwd_blocks(rows);
+    return nl_set_error(NL_EINVAL, std::string(who) + ": need 0 < D <= 4096 and D % 8 == 0");
+  const int nblk = rows > 0 ? ln_bwd_blocks(rows) : 0;
+  if (rows > 0) {
+    if (!dy || !x || !mean || !rstd || !gamma || !dx || !ws)
+      return nl_set_error(NL_EINVAL, std::string(who) + ": null pointer");
+    if ((((uintptr_t)dy | (uintptr_t)x | (uintptr_t)dx | (uintptr_t)dres | (uintptr_t)gamma | (uintptr_t)ws) & 15) != 0)
+      return nl_set_error(NL_EALIGN, std::string(who) + ": buffers must be 16-byte aligned");
+    if (ws_bytes < nl_layernorm_bwd_ws_bytes(rows, D))
+      return nl_set_error(NL_EINVAL, std::string(who) + ": workspace smaller than nl_layernorm_bwd_ws_bytes()");
+  }
+  const int grid = nblk + 2 * prev.strips;
+  if (grid == 0) return NL_OK;
   float* pg = static_cast<float*>(ws);
-  float* pb = pg + (size_t)blocks * D;
+  float* pb = rows > 0 ? pg + (size_t)nblk * D : nullptr;
   hipStream_t st = (hipStream_t)stream;
-  dim3 grid(blocks), block(64 * kRowsPerBlock);
   switch (vectors_per_lane(D)) {
-#define NL_LNB(N)                                                                                                       \
-  case N:                                                                                                               \
-    hipLaunchKernelGGL(ln_bwd_kernel<N>, grid, block, 0, st, rows, D, dy, x, mean, rstd, gamma, dres, dx, pg, pb); \
+#define NL_LNB(N)                                                                                                 \
+  case N:                                                                                                         \
+    hipLaunchKernelGGL(ln_bwd_kernel<N>, dim3(grid), dim3(64 * kRowsPerBlock), 0, st, rows, D, dy, x, mean, rstd, \
+                       gamma, dres, dx, pg, pb, nblk, prev);                                                      \
     break;
     NL_LNB(1)
     NL_LNB(2)
@@ -434,9 +475,69 @@ extern "C" int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy
     NL_LNB(8)
 #undef NL_LNB
   }
-  hipLaunchKernelGGL(sum_partials_kernel, dim3((D + 15) / 16, 2), dim3(256), 0, st, blocks, D, (const float*)pg,
-                     dgamma, (const float*)pb, dbeta, accumulate);
+  return NL_OK;
+}
+
+// The reduction of the partial rows a deferred call left in ws.
+int partial_sums_of(int rows, int D, const void* ws, float* dgamma, float* dbeta, int accumulate, PartialSums& out,
+                    const char* who) {
+  out = no_partial_sums();
+  if (rows <= 0 || !ws) return NL_OK;
+  if (D <= 0 || (D % 8) != 0 || D > kMaxD)
+    return nl_set_error(NL_EINVAL, std::string(who) + ": partial sums need 0 < D <= 4096 and D % 8 == 0");
+  if (!dgamma || !dbeta) return nl_set_error(NL_EINVAL, std::string(who) + ": null dgamma or dbeta");
+  if (((uintptr_t)ws & 15) != 0) return nl_set_error(NL_EALIGN, std::string(who) + ": partials must be 16-byte aligned");
+  out.P = ln_bwd_blocks(rows);
+  out.D = D;
+  out.strips = (D + 15) / 16;
+  out.part_g = static_cast<const float*>(ws);
+  out.part_b = out.part_g + (size_t)out.P * D;
+  out.dgamma = dgamma;
+  out.dbeta = dbeta;
+  out.accumulate = accumulate;
+  return NL_OK;
+}
+}  // namespace
+}  // namespace nl
+
+extern "C" int nl_layernorm_bwd(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x, const float* mean,
+                                const float* rstd, const float* gamma, const nl_bf16* dres, nl_bf16* dx, float* dgamma,
+                                float* dbeta, int accumulate, void* ws, size_t ws_bytes) {
+  if (rows < 0 || D <= 0 || (D % 8) != 0 || D > kMaxD)
+    return nl_set_error(NL_EINVAL, "layernorm: need 0 < D <= 4096 and D % 8 == 0");
+  if (rows == 0) return NL_OK;
+  if (!dgamma || !dbeta) return nl_set_error(NL_EINVAL, "layernorm_bwd: null pointer");
+  NL_TRY(ln_bwd_launch(stream, rows, D, dy, x, mean, rstd, gamma, dres, dx, ws, ws_bytes, no_partial_sums(),
+                       "layernorm_bwd"));
+  const int blocks = ln_bwd_blocks(rows);
+  const float* pg = static_cast<const float*>(ws);
+  hipLaunchKernelGGL(sum_partials_kernel, dim3((D + 15) / 16, 2), dim3(256), 0, (hipStream_t)stream, blocks, D, pg,
+                     dgamma, pg + (size_t)blocks * D, dbeta, accumulate);
   return nl_check_launch("nl_layernorm_bwd");
+}
+
+extern "C" int nl_layernorm_bwd_deferred(void* stream, int rows, int D, const nl_bf16* dy, const nl_bf16* x,
+                                         const float* mean, const float* rstd, const float* gamma,
+                                         const nl_bf16* dres, nl_bf16* dx, void* ws, size_t ws_bytes, int prev_rows,
+                                         int prev_D, const void* prev_ws, float* prev_dgamma, float* prev_dbeta,
+                                         int prev_accumulate) {
+  PartialSums prev;
+  NL_TRY(partial_sums_of(prev_rows, prev_D, prev_ws, prev_dgamma, prev_dbeta, prev_accumulate, prev,
+                         "layernorm_bwd_deferred"));
+  NL_TRY(ln_bwd_launch(stream, rows, D, dy, x, mean, rstd, gamma, dres, dx, ws, ws_bytes, prev,
+                       "layernorm_bwd_deferred"));
+  return nl_check_launch("nl_layernorm_bwd_deferred");
+}
+
+extern "C" int nl_layernorm_param_sums(void* stream, int rows, int D, const void* ws, float* dgamma, float* dbeta,
+                                       int accumulate) {
+  if (rows < 0) return nl_set_error(NL_EINVAL, "layernorm_param_sums: rows < 0");
+  PartialSums ps;
+  NL_TRY(partial_sums_of(rows, D, ws, dgamma, dbeta, accumulate, ps, "layernorm_param_sums"));
+  if (ps.strips == 0) return NL_OK;
+  hipLaunchKernelGGL(sum_partials_kernel, dim3(ps.strips, 2), dim3(256), 0, (hipStream_t)stream, ps.P, ps.D,
+                     ps.part_g, ps.dgamma, ps.part_b, ps.dbeta, accumulate);
+  return nl_check_launch("nl_layernorm_param_sums");
 }
 
 extern "C" size_t nl_colsum_ws_bytes(int rows, int cols) {

@@ -16,6 +16,8 @@ there is no framework fallback.
 """
 from __future__ import annotations
 
+import contextlib
+
 import torch
 
 from .. import _lib
@@ -67,19 +69,61 @@ def layer_norm_fwd_raw(x2, gamma, beta, eps, residual=None):
     return y, s, mean, rstd
 
 
+_ln_defer: dict | None = None   # set inside defer_layer_norm_param_sums()
+
+
+@contextlib.contextmanager
+def defer_layer_norm_param_sums():
+    """Inside the block, a LayerNorm backward that writes dgamma / dbeta into
+    main_grad buffers leaves them as partial rows, which the next such
+    backward's kernel launch reduces (nl_layernorm_bwd_deferred); leaving the
+    block reduces the last ones (nl_layernorm_param_sums). The buffers are
+    complete only after the block, so it belongs around a backward pass whose
+    parameter gradients an optimizer reads afterwards. The sums are the same
+    bit for bit; the chain of 9 LayerNorm backwards loses 8 kernel launches.
+    Module-global like kernels.wgrad (the autograd engine runs the backward
+    on its own thread); one block at a time."""
+    global _ln_defer
+    if _ln_defer is not None:
+        raise RuntimeError("defer_layer_norm_param_sums() does not nest")
+    _ln_defer = {"pending": None}
+    try:
+        yield
+    finally:
+        pending, _ln_defer = _ln_defer["pending"], None
+        if pending is not None:
+            stream, ws, rows, D, dg, db = pending
+            _lib.call("nl_layernorm_param_sums", stream, rows, D, ws.data_ptr(), dg.data_ptr(), db.data_ptr(), 0)
+
+
 def layer_norm_bwd_raw(dy2, xin, mean, rstd, gamma, dres=None, dgamma=None, dbeta=None):
-    """-> dx (+ dres), dgamma, dbeta (written into the given buffers if any)."""
+    """-> dx (+ dres), dgamma, dbeta (written into the given buffers if any;
+    deferred inside ``defer_layer_norm_param_sums`` when both are given)."""
     rows, D = dy2.shape
     dx = torch.empty_like(dy2)
+    wsb = int(_lib.load().nl_layernorm_bwd_ws_bytes(rows, D))
+    ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=dy2.device)
+    dres_ptr = dres.data_ptr() if dres is not None else None
+    if _ln_defer is not None and dgamma is not None and dbeta is not None:
+        prev = _ln_defer["pending"]
+        stream = _stream(dy2)
+        if prev is not None and prev[0] != stream:
+            raise RuntimeError("layer_norm backward: deferred parameter sums on two streams")
+        pargs = (prev[2], prev[3], prev[1].data_ptr(), prev[4].data_ptr(), prev[5].data_ptr(), 0) if prev else \
+            (0, 0, None, None, None, 0)
+        _lib.call("nl_layernorm_bwd_deferred", stream, rows, D, dy2.data_ptr(), xin.data_ptr(), mean.data_ptr(),
+                  rstd.data_ptr(), gamma.data_ptr(), dres_ptr, dx.data_ptr(), ws.data_ptr(), wsb, *pargs)
+        # the previous partials are read by the launch just queued: stream order
+        # keeps their memory from being reused before it runs
+        _ln_defer["pending"] = (stream, ws, rows, D, dgamma, dbeta)
+        return dx, dgamma, dbeta
     if dgamma is None:
         dgamma = torch.empty(D, dtype=_F32, device=dy2.device)
     if dbeta is None:
         dbeta = torch.empty(D, dtype=_F32, device=dy2.device)
-    wsb = int(_lib.load().nl_layernorm_bwd_ws_bytes(rows, D))
-    ws = torch.empty(max(wsb, 16) // 4, dtype=_F32, device=dy2.device)
     _lib.call("nl_layernorm_bwd", _stream(dy2), rows, D, dy2.data_ptr(), xin.data_ptr(), mean.data_ptr(),
-              rstd.data_ptr(), gamma.data_ptr(), dres.data_ptr() if dres is not None else None, dx.data_ptr(),
-              dgamma.data_ptr(), dbeta.data_ptr(), 0, ws.data_ptr(), wsb)
+              rstd.data_ptr(), gamma.data_ptr(), dres_ptr, dx.data_ptr(), dgamma.data_ptr(), dbeta.data_ptr(), 0,
+              ws.data_ptr(), wsb)
     return dx, dgamma, dbeta
 
 

@@ -27,7 +27,7 @@ import torch
 
 from . import _lib
 from .checkpoint import load_checkpoint, load_resume_state, save_checkpoint, save_resume_state  # noqa: F401
-from .kernels import wgrad
+from .kernels import fused, wgrad
 from .kernels.cross_entropy import cross_entropy, linear_cross_entropy
 from .model import (BASELINE, ModelConfig, count_params, init_model, model_forward, model_forward_features,
                     output_projection, tree_leaves)
@@ -257,8 +257,9 @@ def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool =
             p.grad = None
         loss = batch_loss(params, batch, cfg, fused_lmhead)
         # weight gradients run on a second stream beside the dX chain; the
-        # context joins it before the optimizer reads the gradient buffers
-        with overlap(loss.device):
+        # contexts join it and finish the LayerNorm parameter sums before the
+        # optimizer reads the gradient buffers
+        with overlap(loss.device), fused.defer_layer_norm_param_sums():
             loss.backward()
         with torch.no_grad():
             opt_state = optimizer.update(params, opt_state)
@@ -300,7 +301,7 @@ class _GraphedStep:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             loss = batch_loss(params, self.static_batch, self.cfg, self.fused_lmhead)
-            with self.overlap(loss.device):
+            with self.overlap(loss.device), fused.defer_layer_norm_param_sums():
                 loss.backward(seed)
             with torch.no_grad():
                 self.opt.apply(params, state)

@@ -306,3 +306,54 @@ def test_embedding_layer_norm_matches_the_composition(dev, B, S, P):
         # the composition rounds the LayerNorm's dx to bf16 first
         assert rel_l2(g, _np(want.grad)) <= 1e-2
     assert not _np(fused[1].main_grad)[S:].any()
+
+
+@pytest.mark.parametrize("shapes", [[(16384, 512), (16384, 512), (300, 512)], [(257, 512), (33, 1024), (5, 4096)]])
+def test_layernorm_deferred_param_sums_match_bitwise(dev, shapes):
+    """A chain of nl_layernorm_bwd_deferred calls (each launch reducing the previous call's
+    partials) closed by nl_layernorm_param_sums gives the dx, dgamma and dbeta of separate
+    nl_layernorm_bwd calls bit for bit, including an accumulating reduction."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels import fused
+
+    rng = np.random.default_rng(len(shapes) + shapes[-1][0])
+    st = torch.cuda.current_stream(dev).cuda_stream
+    calls = []
+    for rows, D in shapes:
+        x = _dev_bf16(rng.standard_normal((rows, D)), dev)
+        dy = _dev_bf16(rng.standard_normal((rows, D)), dev)
+        g = _f32(1 + 0.1 * rng.standard_normal(D), dev)
+        b = _f32(0.1 * rng.standard_normal(D), dev)
+        _, _, mean, rstd = fused.layer_norm_fwd_raw(x, g, b, 1e-5)
+        calls.append((rows, D, x, dy, g, mean, rstd, _f32(rng.standard_normal(D), dev), _f32(rng.standard_normal(D), dev)))
+    accumulate = [0, 1, 0]
+    plain, chained, keep, pending = [], [], [], None
+    for (rows, D, x, dy, g, mean, rstd, g0, b0), acc in zip(calls, accumulate):
+        wsb = int(_lib.load().nl_layernorm_bwd_ws_bytes(rows, D))
+        outs = []
+        for deferred in (False, True):
+            dx = torch.empty_like(x)
+            dg, db = g0.clone(), b0.clone()
+            ws = torch.empty(wsb // 4, dtype=torch.float32, device=dev)
+            if not deferred:
+                _lib.call("nl_layernorm_bwd", st, rows, D, dy.data_ptr(), x.data_ptr(), mean.data_ptr(),
+                          rstd.data_ptr(), g.data_ptr(), None, dx.data_ptr(), dg.data_ptr(), db.data_ptr(), acc,
+                          ws.data_ptr(), wsb)
+            else:
+                prev = (pending[0], pending[1], pending[2].data_ptr(), pending[3].data_ptr(), pending[4].data_ptr(),
+                        pending[5]) if pending else (0, 0, None, None, None, 0)
+                _lib.call("nl_layernorm_bwd_deferred", st, rows, D, dy.data_ptr(), x.data_ptr(), mean.data_ptr(),
+                          rstd.data_ptr(), g.data_ptr(), None, dx.data_ptr(), ws.data_ptr(), wsb, *prev)
+                keep.append(ws)      # partials stay alive until a later launch has reduced them
+                pending = (rows, D, ws, dg, db, acc)
+            outs.append((dx, dg, db))
+        plain.append(outs[0])
+        chained.append(outs[1])
+    rows, D, ws, dg, db, acc = pending
+    _lib.call("nl_layernorm_param_sums", st, rows, D, ws.data_ptr(), dg.data_ptr(), db.data_ptr(), acc)
+    torch.cuda.synchronize()
+    assert len(chained) == len(plain) == len(shapes)
+    for (dx0, dg0, db0), (dx1, dg1, db1) in zip(plain, chained):
+        assert torch.equal(dx0.view(torch.int16), dx1.view(torch.int16))
+        assert torch.equal(dg0, dg1) and torch.equal(db0, db1)

@@ -61,6 +61,15 @@ def test_status_strings_and_argument_errors_without_gpu():
     assert lib.nl_layernorm_bwd(None, 64, 512, 256, 512, 768, 1024, 1280, None, 1536, 1792, 2048, 0, 2304,
                                 16) == _lib.NL_EINVAL
     assert b"workspace" in lib.nl_last_error()
+    # deferred parameter sums: the same checks, plus those of the earlier call's partials
+    dargs = (None, 64, 512, 256, 512, 768, 1024, 1280, None, 1536, 2304, 64 * 512 * 8)
+    assert lib.nl_layernorm_bwd_deferred(*dargs[:11], 16, 0, 0, None, None, None, 0) == _lib.NL_EINVAL
+    assert b"workspace" in lib.nl_last_error()
+    assert lib.nl_layernorm_bwd_deferred(*dargs, 64, 12, 4096, 512, 768, 0) == _lib.NL_EINVAL
+    assert lib.nl_layernorm_bwd_deferred(*dargs, 64, 512, 4100, 512, 768, 0) == _lib.NL_EALIGN
+    assert lib.nl_layernorm_bwd_deferred(*dargs, 64, 512, 4096, None, 768, 0) == _lib.NL_EINVAL
+    assert lib.nl_layernorm_param_sums(None, 64, 512, 4096, None, 768, 0) == _lib.NL_EINVAL
+    assert lib.nl_layernorm_param_sums(None, 0, 512, None, None, None, 0) == _lib.NL_OK      # nothing to reduce
     assert lib.nl_colsum_ws_bytes(16384, 2048) == 256 * 2048 * 4
     assert lib.nl_colsum_bf16(None, 8, 8, 256, 12, 512, 0, 768, 4096) == _lib.NL_EALIGN
     assert lib.nl_embedding_fwd(None, 2, 8, 6, 100, 256, 512, 768, 1024) == _lib.NL_EINVAL
