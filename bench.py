@@ -280,12 +280,34 @@ def load_traffic(tag: str):
     return k.get("bytes_per_launch") if k else None
 
 
-def gemm_compare(reps: int = 20) -> None:
+def _median_us(fn, n: int = 50, batches: int = 5, warmup: int = 5) -> float:
+    """Kernel-level timing: ``warmup`` untimed calls, then ``batches`` runs of
+    ``n`` back-to-back calls, each bracketed by HIP events on the current
+    stream; the median of the per-call means, in microseconds."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    means = []
+    for _ in range(batches):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        means.append(e0.elapsed_time(e1) / n * 1e3)
+    return float(sorted(means)[len(means) // 2])
+
+
+def gemm_compare(reps: int = 50) -> None:
     """The BASELINE GEMM products (configs[2]: M = 16384 and the model's (K, N),
     each as forward NN, dX = dY.W^T (NT) and dW = X^T.dY (TN)) through this
-    library and through torch.matmul (hipBLASLt), both timed with HIP events
-    on the current stream after warm-up. One JSON line per product. torch's
-    dW comes out in bf16, ours in fp32 as the training step uses it."""
+    library and through torch.matmul (hipBLASLt), both timed by ``_median_us``
+    (median of 5 batches of ``reps`` calls after 5 warm-ups). One JSON line per
+    product. torch's dW comes out in bf16, ours in fp32 as the training step
+    uses it."""
     import torch
 
     from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
@@ -293,18 +315,6 @@ def gemm_compare(reps: int = 20) -> None:
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(0)
     M = 16384
-
-    def timeit(fn, n):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(n):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n * 1e3
 
     for K, N in ((512, 1536), (512, 512), (512, 2048), (2048, 512), (512, 50257)):
         X = torch.randn((M, K), generator=g, device=dev).to(torch.bfloat16)
@@ -314,12 +324,11 @@ def gemm_compare(reps: int = 20) -> None:
         dY.copy_(torch.randn((M, N), generator=g, device=dev))
         Y, dX = padded_empty(M, N, torch.bfloat16, dev), padded_empty(M, K, torch.bfloat16, dev)
         dW = padded_empty(K, N, torch.float32, dev)
-        n = max(3, reps // 4) if N > 4096 else reps
         for lay, ours, lib in (("NN", lambda: gemm_raw(X, W, out=Y), lambda: X @ W),
                                ("NT", lambda: gemm_raw(dY, W, "N", "T", out=dX), lambda: dY @ W.t()),
                                ("TN", lambda: gemm_raw(X, dY, "T", "N", out=dW), lambda: X.t() @ dY)):
             mm, nn, kk = (M, N, K) if lay == "NN" else (M, K, N) if lay == "NT" else (K, N, M)
-            t_ours, t_lib = timeit(ours, n), timeit(lib, n)
+            t_ours, t_lib = _median_us(ours, reps), _median_us(lib, reps)
             fl = 2.0 * mm * nn * kk
             print(json.dumps({"gemm": f"{lay}_{mm}x{nn}x{kk}", "ours_us": round(t_ours, 1),
                               "hipblaslt_us": round(t_lib, 1), "ours_tflops": round(fl / t_ours / 1e6, 1),
@@ -327,13 +336,14 @@ def gemm_compare(reps: int = 20) -> None:
                               "speedup": round(t_lib / t_ours, 3)}), flush=True)
 
 
-def kernel_configs(reps: int = 20) -> None:
+def kernel_configs(reps: int = 50) -> None:
     """BASELINE configs[1] (causal flash forward and backward at (256, 512, 64)
     and (32, 4096, 64), head dim 64, scale 1/8) and configs[3] (CE + dlogits at
     (16384, 50257), logits ~ N(0, 2) bf16) in isolation: this library against
     torch's own kernels for the same work (scaled_dot_product_attention with
-    is_causal, and cross_entropy forward + backward), HIP events on the current
-    stream after warm-up. One JSON line per case with the roofline fraction."""
+    is_causal, and cross_entropy forward + backward), timed by ``_median_us``
+    (median of 5 batches of ``reps`` calls after 5 warm-ups). One JSON line per
+    case with the roofline fraction."""
     import torch
 
     from nlearn_amd.attention import flash_bwd_raw4, flash_fwd_raw4
@@ -343,16 +353,7 @@ def kernel_configs(reps: int = 20) -> None:
     g = torch.Generator(device=dev).manual_seed(0)
 
     def timeit(fn, n=reps):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(n):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / n * 1e3
+        return _median_us(fn, n)
 
     for n, S in ((256, 512), (32, 4096)):
         B, H = n // 8, 8
@@ -374,14 +375,14 @@ def kernel_configs(reps: int = 20) -> None:
     M, V = 16384, 50257
     logits = (torch.randn((M, V), generator=g, device=dev) * 2.0).to(torch.bfloat16)
     t = torch.randint(0, V, (M,), generator=g, device=dev)
-    t_o = timeit(lambda: ce_fwd_bwd_raw(logits, t), max(3, reps // 4))
+    t_o = timeit(lambda: ce_fwd_bwd_raw(logits, t))
     lr = logits.detach().clone().requires_grad_(True)
 
     def torch_ce():
         loss = torch.nn.functional.cross_entropy(lr, t)
         return torch.autograd.grad(loss, lr)
 
-    t_t = timeit(torch_ce, max(3, reps // 4))
+    t_t = timeit(torch_ce)
     byt = 4.0 * M * V + 12.0 * M
     print(json.dumps({"case": f"ce_fwd_bwd_{M}x{V}", "ours_us": round(t_o, 1), "torch_us": round(t_t, 1),
                       "ours_frac": round(byt / t_o / 1e3 / PEAK_HBM_GBS, 4),
@@ -394,7 +395,7 @@ def kernel_configs(reps: int = 20) -> None:
     dst = torch.empty_like(src)
     for tag, fn, byt in (("hbm_copy_2GiB", lambda: dst.copy_(src), 8.0 * n), ("hbm_fill_2GiB", lambda: dst.fill_(1.0), 4.0 * n),
                          ("hbm_sum_2GiB", lambda: src.sum(), 4.0 * n)):
-        t_x = timeit(fn, 10)
+        t_x = timeit(fn)
         print(json.dumps({"case": tag, "torch_us": round(t_x, 1), "tbs": round(byt / t_x / 1e6, 3),
                           "torch_frac": round(byt / t_x / 1e3 / PEAK_HBM_GBS, 4)}), flush=True)
 
