@@ -204,6 +204,32 @@ int nl_flash_attention_bwd(void* stream, int batch, int heads, int seq, int d_he
                            nl_bf16* dV, nl_attn_stride sdv,
                            void* ws);
 
+/* nl_flash_attention_bwd without a workspace argument: D lives in a fixed
+ * device array inside this library (NL_FLASH_BWD_NOALLOC_MAX_ROWS floats,
+ * 8 MiB, held by every GPU the library runs on until the process ends), so the
+ * call allocates nothing and needs nothing from the caller beyond inputs and
+ * outputs. It has no counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). batch*heads*seq above the maximum returns
+ * NL_EINVAL before anything is launched. The stream must belong to the
+ * current device; the first call on a device resolves the array's address
+ * there (make it before any graph capture). All calls on one GPU share the
+ * array: calls that overlap in time on one GPU (two streams, two threads)
+ * race on D and must be serialised by the caller. Results are those of
+ * nl_flash_attention_bwd, bit for bit. */
+#define NL_FLASH_BWD_NOALLOC_MAX_ROWS 2097152
+int nl_flash_attention_bwd_noalloc(void* stream, int batch, int heads, int seq, int d_head,
+                                   float scale, int causal,
+                                   const nl_bf16* Q, nl_attn_stride sq,
+                                   const nl_bf16* K, nl_attn_stride sk,
+                                   const nl_bf16* V, nl_attn_stride sv,
+                                   const nl_bf16* O, nl_attn_stride so,
+                                   const nl_bf16* dO, nl_attn_stride sdo,
+                                   const float* L,
+                                   nl_bf16* dQ, nl_attn_stride sdq,
+                                   nl_bf16* dK, nl_attn_stride sdk,
+                                   nl_bf16* dV, nl_attn_stride sdv);
+
 /* ======================================================================== */
 /* Softmax cross-entropy                                                      */
 /* ======================================================================== */

@@ -61,6 +61,8 @@ _SIGNATURES = {
     "nl_flash_attention_bwd_ws_bytes": [_I, _I, _I],
     "nl_flash_attention_bwd": [_P, _I, _I, _I, _I, _F, _I, _P, _S, _P, _S, _P, _S, _P, _S, _P, _S, _P,
                                _P, _S, _P, _S, _P, _S, _P],
+    "nl_flash_attention_bwd_noalloc": [_P, _I, _I, _I, _I, _F, _I, _P, _S, _P, _S, _P, _S, _P, _S, _P, _S, _P,
+                                       _P, _S, _P, _S, _P, _S],
     "nl_ce_fwd": [_P, _I, _I, _P, _I64, _P, _P, _P],
     "nl_ce_bwd": [_P, _I, _I, _P, _I64, _P, _P, _F, _P, _I64],
     "nl_ce_fwd_bwd": [_P, _I, _I, _P, _I64, _P, _P, _P, _F, _P, _I64],

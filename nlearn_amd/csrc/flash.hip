@@ -29,6 +29,8 @@
 //   * Causal work skipping per wave; fully masked waves only join the barriers.
 //     The heaviest tiles are launched first.
 #include <type_traits>
+#include <atomic>
+#include <mutex>
 
 #include "common.h"
 
@@ -824,4 +826,64 @@ extern "C" int nl_flash_attention_bwd(void* stream, int batch, int heads, int se
   NL_TRY(nl_flash_attention_bwd_dq(stream, batch, heads, seq, d_head, scale, causal, Q, sq, K, sk, V, sv, dO, sdo,
                                    L, D, dQ, sdq));
   return NL_OK;
+}
+
+// ---------------------------------------------------------------------------
+// The backward without a caller workspace: D lives in a fixed device array.
+// ---------------------------------------------------------------------------
+// The array is a per-device global of the code object (each GPU holds its own
+// copy, at its own address, until the process ends). Its host-side name is
+// only a handle: kernels must be given the device address that
+// hipGetSymbolAddress returns, looked up once per device and cached here.
+static __device__ __align__(256) float scratch[NL_FLASH_BWD_NOALLOC_MAX_ROWS];
+
+namespace nl {
+namespace {
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (first call per device
+// resolves it with that device current).
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return nl_set_error(NL_ELAUNCH, std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return nl_set_error(NL_EUNSUPPORTED, "flash noalloc: device index >= 64");
+  float* p = g_scratch_dev[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_dev[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      void* addr = nullptr;
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess || !addr)
+        return nl_set_error(NL_ELAUNCH, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+      p = static_cast<float*>(addr);
+      g_scratch_dev[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return NL_OK;
+}
+}  // namespace
+}  // namespace nl
+
+extern "C" int nl_flash_attention_bwd_noalloc(void* stream, int batch, int heads, int seq, int d_head, float scale,
+                                              int causal, const nl_bf16* Q, nl_attn_stride sq, const nl_bf16* K,
+                                              nl_attn_stride sk, const nl_bf16* V, nl_attn_stride sv,
+                                              const nl_bf16* O, nl_attn_stride so, const nl_bf16* dO,
+                                              nl_attn_stride sdo, const float* L, nl_bf16* dQ, nl_attn_stride sdq,
+                                              nl_bf16* dK, nl_attn_stride sdk, nl_bf16* dV, nl_attn_stride sdv) {
+  NL_TRY(check_common(batch, heads, seq, d_head, causal));
+  if (batch == 0 || heads == 0 || seq == 0) return NL_OK;
+  if ((int64_t)batch * heads * seq > (int64_t)NL_FLASH_BWD_NOALLOC_MAX_ROWS)
+    return nl_set_error(NL_EINVAL, "flash noalloc: batch*heads*seq exceeds NL_FLASH_BWD_NOALLOC_MAX_ROWS (" +
+                                       std::to_string(NL_FLASH_BWD_NOALLOC_MAX_ROWS) + ")");
+  float* D = nullptr;
+  NL_TRY(scratch_on_current_device(&D));
+  // D is written whole by the preprocess before dK/dV and dQ read it, so the
+  // array needs no clearing between calls.
+  return nl_flash_attention_bwd(stream, batch, heads, seq, d_head, scale, causal, Q, sq, K, sk, V, sv, O, so, dO, sdo,
+                                L, dQ, sdq, dK, sdk, dV, sdv, D);
 }
