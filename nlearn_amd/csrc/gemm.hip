@@ -29,8 +29,9 @@
 //   * MFMA operands are swapped (B fragment as src A) so every lane ends up with
 //     4 consecutive output columns: 16-byte fp32 / 8-byte bf16 stores.
 //   * A ragged K tail is staged through registers with element masks.
-// The first-generation register-staged kernel (gemm_kernel) remains as the
-// path for operands beyond the 2 GB reach of 32-bit buffer offsets.
+//   * Operands beyond the 2 GB reach of 32-bit buffer offsets are split on the
+//     host into sub-products that fit it (panels of M or N; chunks of K summed
+//     in the fp32 output).
 #include "common.h"
 
 namespace nl {
@@ -98,83 +99,6 @@ __device__ __forceinline__ u32x4 load8(const uint16_t* p, int lim) {
   return r;
 }
 
-// Stage loader for one operand tile of ROWS (m or n) x BK (k).
-//   KMAJ:  element (row, k) at P[row * ld + k]   (k contiguous)
-//   !KMAJ: element (row, k) at P[k * ld + row]   (row contiguous)
-template <int ROWS, int NT, bool KMAJ>
-struct TileLoader {
-  // K-major: ROWS*CHUNKS chunks; MN-major: (BK/8)*(ROWS/8) 8x8 blocks (8 loads each)
-  static constexpr int UNITS = KMAJ ? ROWS * CHUNKS : (BK / 8) * (ROWS / 8);
-  static constexpr int PER = (UNITS + NT - 1) / NT;
-  static constexpr int REGS = KMAJ ? PER : PER * 8;
-  u32x4 r[REGS];
-
-  __device__ __forceinline__ void load(const uint16_t* __restrict__ P, int64_t ld, int row0, int rows_lim, int k0,
-                                       int k_lim, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = i * NT + tid;
-      if (UNITS % NT == 0 || u < UNITS) {
-        if constexpr (KMAJ) {
-          const int row = u / CHUNKS, kc = u % CHUNKS;
-          const int grow = row0 + row, gk = k0 + kc * 8;
-          if (grow < rows_lim) r[i] = load8(P + (int64_t)grow * ld + gk, k_lim - gk);
-          else r[i] = u32x4{0u, 0u, 0u, 0u};
-        } else {
-          const int kb = u / (ROWS / 8), rb = u % (ROWS / 8);
-          const int grow = row0 + rb * 8;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const int gk = k0 + kb * 8 + q;
-            if (gk < k_lim) r[i * 8 + q] = load8(P + (int64_t)gk * ld + grow, rows_lim - grow);
-            else r[i * 8 + q] = u32x4{0u, 0u, 0u, 0u};
-          }
-        }
-      }
-    }
-  }
-
-  // Interior tile, full k stage: no bounds checks at all.
-  __device__ __forceinline__ void load_fast(const uint16_t* __restrict__ P, int64_t ld, int row0, int k0, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = i * NT + tid;
-      if (UNITS % NT == 0 || u < UNITS) {
-        if constexpr (KMAJ) {
-          const int row = u / CHUNKS, kc = u % CHUNKS;
-          r[i] = *reinterpret_cast<const u32x4*>(P + (int64_t)(row0 + row) * ld + k0 + kc * 8);
-        } else {
-          const int kb = u / (ROWS / 8), rb = u % (ROWS / 8);
-          const uint16_t* base = P + (int64_t)(k0 + kb * 8) * ld + row0 + rb * 8;
-#pragma unroll
-          for (int q = 0; q < 8; ++q) r[i * 8 + q] = *reinterpret_cast<const u32x4*>(base + (int64_t)q * ld);
-        }
-      }
-    }
-  }
-
-  __device__ __forceinline__ void store(uint16_t* __restrict__ S, int tid) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int u = i * NT + tid;
-      if (UNITS % NT == 0 || u < UNITS) {
-        if constexpr (KMAJ) {
-          const int row = u / CHUNKS, kc = u % CHUNKS;
-          *reinterpret_cast<u32x4*>(S + row * BK + swz(row, kc) * 8) = r[i];
-        } else {
-          const int kb = u / (ROWS / 8), rb = u % (ROWS / 8);
-          u32x4 t[8];
-          transpose8x8_b16(&r[i * 8], t);
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            const int row = rb * 8 + c;
-            *reinterpret_cast<u32x4*>(S + row * BK + swz(row, kb) * 8) = t[c];
-          }
-        }
-      }
-    }
-  }
-};
 
 template <typename OutT>
 __device__ __forceinline__ void store4(OutT* c, float v0, float v1, float v2, float v3);
@@ -283,170 +207,6 @@ __device__ __forceinline__ void epilogue4_any(const GemmArgs& g, int64_t m, int 
     case NL_EPI_BIAS_GELU: epilogue_apply<OutT, NL_EPI_BIAS_GELU>(g, m, n, v, b, a); break;
     case NL_EPI_DGELU: epilogue_apply<OutT, NL_EPI_DGELU>(g, m, n, v, b, a); break;
     default: epilogue_apply<OutT, NL_EPI_NONE>(g, m, n, v, b, a); break;
-  }
-}
-
-template <int BM, int BN, int WM, int WN, bool A_KMAJ, bool B_KMAJ, typename OutT>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
-  constexpr int NT = WM * WN * 64;
-  constexpr int WTM = BM / WM, WTN = BN / WN;
-  constexpr int FM = WTM / 32, FN = WTN / 32;
-  static_assert(FM >= 1 && FN >= 1, "wave tile must be >= 32x32");
-
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][(BM + BN) * BK];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
-
-  // Workgroups are dispatched round-robin over the 8 XCDs (each with its own
-  // L2): give every XCD a contiguous run of logical ids, then walk tiles in
-  // groups of 8 M-tiles so the ~32 tiles an XCD runs at once share A and B panels.
-  int bid = blockIdx.x;
-  {
-    const int nwg = gridDim.x, per = nwg / 8;
-    if (bid < per * 8) bid = (bid % 8) * per + bid / 8;
-  }
-  const int tiles_n = (g.N + BN - 1) / BN;
-  const int tiles_m = (g.M + BM - 1) / BM;
-  const int split = bid / g.tiles;
-  const int tile = bid - split * g.tiles;
-  constexpr int GM = 8;
-  const int in_group = GM * tiles_n;
-  const int first_m = (tile / in_group) * GM;
-  const int gsize = min(tiles_m - first_m, GM);
-  const int tm = first_m + (tile % in_group) % gsize;
-  const int tn = (tile % in_group) / gsize;
-  const int m0 = tm * BM, n0 = tn * BN;
-  const int kbeg = split * g.k_chunk;
-  const int kend = min(g.K, kbeg + g.k_chunk);
-  const bool full_mn = (m0 + BM <= g.M) && (n0 + BN <= g.N);
-
-  TileLoader<BM, NT, A_KMAJ> la;
-  TileLoader<BN, NT, B_KMAJ> lb;
-
-  f32x16 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  auto load_stage = [&](int k0) {
-    if (full_mn && k0 + BK <= kend) {
-      la.load_fast(g.A, g.lda, m0, k0, tid);
-      lb.load_fast(g.B, g.ldb, n0, k0, tid);
-    } else {
-      la.load(g.A, g.lda, m0, g.M, k0, kend, tid);
-      lb.load(g.B, g.ldb, n0, g.N, k0, kend, tid);
-    }
-  };
-
-  const int frow = lane & 31;   // row within a 32-row fragment
-  const int fkc = lane >> 5;    // which 8-k half of a 16-k step
-  // per-lane LDS row offsets (elements) and swizzle keys of the fragment rows
-  int aoff[FM], asw[FM], boff[FN], bsw[FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int row = wm * WTM + i * 32 + frow;
-    aoff[i] = row * BK;
-    asw[i] = (row ^ (row >> 3)) & 7;
-  }
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int row = wn * WTN + j * 32 + frow;
-    boff[j] = BM * BK + row * BK;
-    bsw[j] = (row ^ (row >> 3)) & 7;
-  }
-  bf16x8 af[2][FM], bfr[2][FN];
-  auto load_frags = [&](const uint16_t* sb, int ks, int slot) {
-    const int kc = ks * 2 + fkc;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-      af[slot][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + aoff[i] + ((kc ^ asw[i]) << 3)));
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
-      bfr[slot][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(sb + boff[j] + ((kc ^ bsw[j]) << 3)));
-  };
-
-  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  if (nk > 0) {
-    load_stage(kbeg);
-    la.store(smem[0], tid);
-    lb.store(smem[0] + BM * BK, tid);
-    __syncthreads();
-    load_frags(smem[0], 0, 0);
-  }
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    const bool more = (kt + 1) < nk;
-    if (more) load_stage(kbeg + (kt + 1) * BK);
-    const uint16_t* sb = smem[buf];
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < BK / 16) load_frags(sb, ks + 1, cur ^ 1);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j) acc[i][j] = mfma32(bfr[cur][j], af[cur][i], acc[i][j]);
-      if (ks + 1 < BK / 16) {
-        // interleave the next sub-step's fragment reads with this sub-step's MFMAs
-#pragma unroll
-        for (int x = 0; x < FM + FN; ++x) {
-          __builtin_amdgcn_sched_group_barrier(0x008, (FM * FN) / (FM + FN) > 0 ? (FM * FN) / (FM + FN) : 1, 0);
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-      }
-    }
-    if (more) {
-      la.store(smem[buf ^ 1], tid);
-      lb.store(smem[buf ^ 1] + BM * BK, tid);
-    }
-    __syncthreads();
-    if (more) load_frags(smem[buf ^ 1], 0, 0);
-  }
-
-  const int g4 = (lane >> 5) * 4;
-  if (g.ws) {  // split-K partial: raw fp32 sums, reduced by splitk_reduce_kernel
-    float* W = g.ws + (int64_t)split * g.M * g.ldw;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int m = m0 + wm * WTM + i * 32 + frow;
-      if (m >= g.M) continue;
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
-          if (n < g.N)  // ldw is a multiple of 4 >= N: the 4-wide store stays in the row
-            *reinterpret_cast<f32x4*>(W + (int64_t)m * g.ldw + n) =
-                f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
-        }
-    }
-    return;
-  }
-  // epilogue: lane holds C[m][n..n+3] for m = row of lane, n = 8q + 4*(lane/32)
-  float s = g.alpha;
-  if (g.alpha_dev) s *= *g.alpha_dev;
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int m = m0 + wm * WTM + i * 32 + frow;
-    if (m >= g.M) continue;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int n = n0 + wn * WTN + j * 32 + q * 8 + g4;
-        if (n >= g.N) continue;
-        float v[4] = {acc[i][j][4 * q + 0] * s, acc[i][j][4 * q + 1] * s, acc[i][j][4 * q + 2] * s,
-                      acc[i][j][4 * q + 3] * s};
-        epilogue4_any<OutT>(g, m, n, v);
-      }
-    }
   }
 }
 
@@ -1438,24 +1198,10 @@ Plan make_plan(int opA, int opB, int M, int N, int K, int epi) {
   return p;
 }
 
-template <int BM, int BN, int WM, int WN, bool AK, bool BK_, typename OutT>
-void launch_cfg(GemmArgs g, const Plan& plan, hipStream_t st) {
-  Plan p = plan;
-  // the v2 kernel addresses operands with 32-bit buffer offsets
-  // (rows up to a 256-row tile past the end, which the range check zeroes)
-  const int64_t a_ext = (AK ? (int64_t)g.M + 256 : (int64_t)g.K + BK) * g.lda * 2;
-  const int64_t b_ext = (BK_ ? (int64_t)g.N + 256 : (int64_t)g.K + BK) * g.ldb * 2;
-  // (the DGELU epilogue also reads its aux tile through a buffer descriptor)
-  const int64_t aux_ext = g.epi == NL_EPI_DGELU ? ((int64_t)g.M + BM) * g.ldaux * 2 : 0;
-  const bool v2 = WM == 2 && WN == 2 && a_ext < ((int64_t)1 << 31) && b_ext < ((int64_t)1 << 31) &&
-                  aux_ext < ((int64_t)1 << 31);
-  if (p.big && !v2) {  // the register-staged kernel only has 128 x 128 tiles (and no split plan here)
-    p.big = 0;
-    p.tiles = (int)((int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128));
-    p.splits = 1;
-    p.k_chunk = g.K > 0 ? g.K : 1;
-    g.ws = nullptr;
-  }
+// Launch one product whose operands fit 32-bit buffer offsets (the caller,
+// run_product, splits anything larger).
+template <bool AK, bool BK_, typename OutT>
+void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
   g.tiles = p.tiles;
   g.k_chunk = p.k_chunk;
   // Pipeline choice measured on MI355X at the model's shapes: with both
@@ -1504,33 +1250,116 @@ void launch_cfg(GemmArgs g, const Plan& plan, hipStream_t st) {
   };
   if (p.splits > 1) {
     g.ldw = p.ldw;  // g.ws already set by the caller
-    if (v2)
-      launch2(p.tiles * p.splits);
-    else
-      hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles * p.splits), dim3(WM * WN * 64),
-                         0, st, g);
+    launch2(p.tiles * p.splits);
     const int64_t work = (int64_t)g.M * ((g.N + 3) / 4);
     const int blocks = (int)std::min<int64_t>((work + 255) / 256, 4096);
     hipLaunchKernelGGL((splitk_reduce_kernel<OutT>), dim3(blocks), dim3(256), 0, st, g, p.splits);
   } else {
     g.ws = nullptr;
-    if (v2) launch2(p.tiles);
-    else hipLaunchKernelGGL((gemm_kernel<BM, BN, WM, WN, AK, BK_, OutT>), dim3(p.tiles), dim3(WM * WN * 64), 0, st, g);
+    launch2(p.tiles);
   }
-}
-
-template <bool AK, bool BK_, typename OutT>
-void launch_layout(const GemmArgs& g, const Plan& p, hipStream_t st) {
-  launch_cfg<128, 128, 2, 2, AK, BK_, OutT>(g, p, st);
 }
 
 template <typename OutT>
 void launch_typed(int opA, int opB, const GemmArgs& g, const Plan& p, hipStream_t st) {
   // A is k-major when not transposed; B is k-major when transposed.
-  if (opA == NL_OP_N && opB == NL_OP_N) launch_layout<true, false, OutT>(g, p, st);
-  else if (opA == NL_OP_N && opB == NL_OP_T) launch_layout<true, true, OutT>(g, p, st);
-  else if (opA == NL_OP_T && opB == NL_OP_N) launch_layout<false, false, OutT>(g, p, st);
-  else launch_layout<false, true, OutT>(g, p, st);
+  if (opA == NL_OP_N && opB == NL_OP_N) launch_cfg<true, false, OutT>(g, p, st);
+  else if (opA == NL_OP_N && opB == NL_OP_T) launch_cfg<true, true, OutT>(g, p, st);
+  else if (opA == NL_OP_T && opB == NL_OP_N) launch_cfg<false, false, OutT>(g, p, st);
+  else launch_cfg<false, true, OutT>(g, p, st);
+}
+
+// ---------------------------------------------------------------------------
+// Products beyond the reach of 32-bit buffer offsets
+// ---------------------------------------------------------------------------
+// The kernels address each operand (and the DGELU aux) through a buffer
+// descriptor with 32-bit byte offsets, reading up to one tile past the end
+// (the range check zeroes those rows). A product whose operand extent reaches
+// 2 GB is cut into sub-products that each fit, run in order on the stream:
+//   * a k-contiguous A (or the aux) too long in M: panels of rows of C;
+//   * a k-contiguous B too long in N: panels of columns of C;
+//   * a k-strided A or B (stored [K][ld]) too long in K: chunks of K, the
+//     later chunks added into C with beta = 1 (fp32 C, no GELU epilogue;
+//     a bias is added by the first chunk only).
+// Panels are balanced and rounded to whole 256-row tiles; K chunks to 64.
+constexpr int64_t kOffsetLimit = (int64_t)1 << 31;
+
+// rows per panel so that (rows + slack) * row_bytes stays below 2 GB, for a
+// dimension of `total` rows cut into as few balanced panels as possible
+int64_t panel_rows(int64_t total, int64_t row_bytes, int64_t slack, int64_t quantum) {
+  int64_t cap = kOffsetLimit / row_bytes - slack - 1;
+  cap = cap / quantum * quantum;
+  if (cap < quantum) return 0;
+  const int64_t panels = (total + cap - 1) / cap;
+  int64_t per = (total + panels - 1) / panels;
+  return (per + quantum - 1) / quantum * quantum;
+}
+
+// Calls f(sub) for every sub-product of g in launch order; f returns a status.
+template <class F>
+int for_each_subproduct(int opA, int opB, const GemmArgs& g, int c_dtype, F&& f) {
+  const bool AK = opA == NL_OP_N, BKM = opB == NL_OP_T;
+  const int64_t esz = c_dtype == NL_DTYPE_F32 ? 4 : 2;
+  const int64_t aux_ld = g.epi == NL_EPI_DGELU ? g.ldaux : 0;
+  const int64_t m_row_bytes = std::max<int64_t>(AK ? g.lda * 2 : 0, aux_ld * 2);
+  if (g.M > 256 && m_row_bytes > 0 && ((int64_t)g.M + 256) * m_row_bytes >= kOffsetLimit) {
+    const int64_t per = panel_rows(g.M, m_row_bytes, 256, 256);
+    if (per == 0) return nl_set_error(NL_EUNSUPPORTED, "gemm: one 256-row panel of A spans 2 GB");
+    for (int64_t m0 = 0; m0 < g.M; m0 += per) {
+      GemmArgs s = g;
+      s.M = (int)std::min<int64_t>(per, g.M - m0);
+      s.A = AK ? g.A + m0 * g.lda : g.A + m0;
+      s.C = static_cast<char*>(g.C) + m0 * g.ldc * esz;
+      if (g.aux) s.aux = g.aux + m0 * g.ldaux;
+      int rc = for_each_subproduct(opA, opB, s, c_dtype, f);
+      if (rc) return rc;
+    }
+    return NL_OK;
+  }
+  if (BKM && g.N > 256 && ((int64_t)g.N + 256) * g.ldb * 2 >= kOffsetLimit) {
+    const int64_t per = panel_rows(g.N, g.ldb * 2, 256, 256);
+    if (per == 0) return nl_set_error(NL_EUNSUPPORTED, "gemm: one 256-row panel of B spans 2 GB");
+    for (int64_t n0 = 0; n0 < g.N; n0 += per) {
+      GemmArgs s = g;
+      s.N = (int)std::min<int64_t>(per, g.N - n0);
+      s.B = g.B + n0 * g.ldb;
+      s.C = static_cast<char*>(g.C) + n0 * esz;
+      if (g.bias) s.bias = g.bias + n0;
+      if (g.aux) s.aux = g.aux + n0;
+      int rc = for_each_subproduct(opA, opB, s, c_dtype, f);
+      if (rc) return rc;
+    }
+    return NL_OK;
+  }
+  const int64_t k_row_bytes = std::max<int64_t>(AK ? 0 : g.lda * 2, BKM ? 0 : g.ldb * 2);
+  if (g.K > BK && k_row_bytes > 0 && ((int64_t)g.K + BK) * k_row_bytes >= kOffsetLimit) {
+    if (c_dtype != NL_DTYPE_F32 || (g.epi != NL_EPI_NONE && g.epi != NL_EPI_BIAS))
+      return nl_set_error(NL_EUNSUPPORTED,
+                          "gemm: a k-strided operand spanning 2 GB needs an fp32 C and no GELU epilogue");
+    const int64_t per = panel_rows(g.K, k_row_bytes, BK, BK);
+    if (per == 0) return nl_set_error(NL_EUNSUPPORTED, "gemm: 64 rows of a k-strided operand span 2 GB");
+    for (int64_t k0 = 0; k0 < g.K; k0 += per) {
+      GemmArgs s = g;
+      s.K = (int)std::min<int64_t>(per, g.K - k0);
+      s.A = AK ? g.A + k0 : g.A + k0 * g.lda;
+      s.B = BKM ? g.B + k0 : g.B + k0 * g.ldb;
+      if (k0 > 0) {
+        s.beta = 1.f;
+        s.epi = NL_EPI_NONE;
+        s.bias = nullptr;
+      }
+      int rc = for_each_subproduct(opA, opB, s, c_dtype, f);
+      if (rc) return rc;
+    }
+    return NL_OK;
+  }
+  // what is left must fit (a single tile's rows may still be too wide)
+  const int64_t a_ext = (AK ? (int64_t)g.M + 256 : (int64_t)g.K + BK) * g.lda * 2;
+  const int64_t b_ext = (BKM ? (int64_t)g.N + 256 : (int64_t)g.K + BK) * g.ldb * 2;
+  const int64_t x_ext = ((int64_t)g.M + 256) * aux_ld * 2;
+  if (a_ext >= kOffsetLimit || b_ext >= kOffsetLimit || x_ext >= kOffsetLimit)
+    return nl_set_error(NL_EUNSUPPORTED, "gemm: rows of an operand too long for 32-bit buffer offsets");
+  return f(g);
 }
 
 // ---------------------------------------------------------------------------
@@ -1659,7 +1488,23 @@ extern "C" int nl_lce_bwd_dlogits(void* stream, int M, int D, int V, int v0, int
 
 extern "C" size_t nl_gemm_ws_bytes(int opA, int opB, int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0) return 0;
-  return make_plan(opA, opB, M, N, K, NL_EPI_NONE).ws_bytes;
+  if ((opA != NL_OP_N && opA != NL_OP_T) || (opB != NL_OP_N && opB != NL_OP_T)) return 0;
+  // the largest split workspace of the sub-products the call will run, for
+  // dense operands (leading dimensions rounded up to 8)
+  GemmArgs g{};
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  g.lda = ((opA == NL_OP_N ? (int64_t)K : M) + 7) / 8 * 8;
+  g.ldb = ((opB == NL_OP_N ? (int64_t)N : K) + 7) / 8 * 8;
+  g.ldc = ((int64_t)N + 7) / 8 * 8;
+  g.epi = NL_EPI_NONE;
+  size_t most = make_plan(opA, opB, M, N, K, NL_EPI_NONE).ws_bytes;
+  for_each_subproduct(opA, opB, g, NL_DTYPE_F32, [&](const GemmArgs& s) {
+    most = std::max(most, make_plan(opA, opB, s.M, s.N, s.K, NL_EPI_NONE).ws_bytes);
+    return NL_OK;
+  });
+  return most;
 }
 
 extern "C" int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K, float alpha, const nl_bf16* A,
@@ -1690,7 +1535,7 @@ extern "C" int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K
     if (beta != 0.f) return nl_set_error(NL_EINVAL, "gemm: GELU epilogues need beta == 0");
   }
 
-  GemmArgs g;
+  GemmArgs g{};
   g.M = M;
   g.N = N;
   g.K = K;
@@ -1707,17 +1552,25 @@ extern "C" int nl_gemm_fused(void* stream, int opA, int opB, int M, int N, int K
   g.bias = bias;
   g.aux = aux;
   g.ldaux = ldaux;
-  Plan p = make_plan(opA, opB, M, N, K, epi);
-  if (p.splits > 1 && (!ws || ws_bytes < p.ws_bytes || ((uintptr_t)ws & 15) != 0)) {
-    // no (usable) workspace: one workgroup per tile over the whole K range
-    p.splits = 1;
-    p.k_chunk = K > 0 ? K : 1;
-    p.ws_bytes = 0;
-  }
-  g.ws = static_cast<float*>(ws);
   hipStream_t st = (hipStream_t)stream;
-  if (c_dtype == NL_DTYPE_F32) launch_typed<float>(opA, opB, g, p, st);
-  else launch_typed<uint16_t>(opA, opB, g, p, st);
+  // validate the whole decomposition before launching any part of it
+  int rc = for_each_subproduct(opA, opB, g, c_dtype, [](const GemmArgs&) { return NL_OK; });
+  if (rc) return rc;
+  rc = for_each_subproduct(opA, opB, g, c_dtype, [&](const GemmArgs& s) {
+    Plan p = make_plan(opA, opB, s.M, s.N, s.K, s.epi);
+    if (p.splits > 1 && (!ws || ws_bytes < p.ws_bytes || ((uintptr_t)ws & 15) != 0)) {
+      // no (usable) workspace: one workgroup per tile over the whole K range
+      p.splits = 1;
+      p.k_chunk = s.K > 0 ? s.K : 1;
+      p.ws_bytes = 0;
+    }
+    GemmArgs t = s;
+    t.ws = static_cast<float*>(ws);
+    if (c_dtype == NL_DTYPE_F32) launch_typed<float>(opA, opB, t, p, st);
+    else launch_typed<uint16_t>(opA, opB, t, p, st);
+    return NL_OK;
+  });
+  if (rc) return rc;
   return nl_check_launch("nl_gemm");
 }
 

@@ -38,6 +38,8 @@ def _as_rows(logits: torch.Tensor) -> torch.Tensor:
     x = logits.reshape(-1, V)
     if x.stride(-1) != 1:
         raise ValueError("cross_entropy: logits need a unit stride along the vocabulary")
+    if x.shape[0] > 1 and x.stride(0) < V:  # rows sharing memory (a broadcast view)
+        x = x.contiguous()
     return x
 
 

@@ -35,13 +35,22 @@ def _check_device(*ts):
             raise RuntimeError("nlearn_amd kernels need HIP device tensors (got a CPU tensor)")
 
 
+def _rows_disjoint(t: torch.Tensor) -> bool:
+    """True when no two rows of a 2-D view share memory (row stride >= row
+    length). A broadcast view (row stride 0, e.g. the cotangent of a sum over
+    rows) is not: the kernels would read or write past its one stored row."""
+    return t.shape[0] <= 1 or t.stride(0) >= t.shape[1]
+
+
 def _ld(t: torch.Tensor) -> int:
-    """Leading dimension of a row-major 2-D view (unit column stride required)."""
+    """Leading dimension of a row-major 2-D view (unit column stride, disjoint rows)."""
     if t.dim() != 2:
         raise ValueError(f"expected a 2-D tensor, got shape {tuple(t.shape)}")
     if t.stride(1) != 1 and t.shape[1] > 1:
         raise ValueError("GEMM operands need a unit column stride")
-    return max(t.stride(0), t.shape[1]) if t.shape[0] > 1 else (t.shape[1] + 7) // 8 * 8
+    if not _rows_disjoint(t):
+        raise ValueError(f"GEMM operand rows overlap (row stride {t.stride(0)} < row length {t.shape[1]})")
+    return t.stride(0) if t.shape[0] > 1 else (t.shape[1] + 7) // 8 * 8
 
 
 def _aligned(t: torch.Tensor) -> bool:
@@ -49,10 +58,10 @@ def _aligned(t: torch.Tensor) -> bool:
 
 
 def _kernel_ready(t: torch.Tensor) -> torch.Tensor:
-    """bf16, unit column stride, 16-byte aligned rows; copies only when it must."""
+    """bf16, unit column stride, disjoint 16-byte aligned rows; copies only when it must."""
     if t.dtype != _BF16:
         t = t.to(_BF16)
-    if t.dim() == 2 and (t.stride(1) == 1 or t.shape[1] <= 1) and _aligned(t):
+    if t.dim() == 2 and (t.stride(1) == 1 or t.shape[1] <= 1) and _rows_disjoint(t) and _aligned(t):
         return t
     rows, cols = t.shape
     ld = (cols + 7) // 8 * 8
