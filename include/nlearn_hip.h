@@ -309,12 +309,15 @@ int nl_scale_bf16_by_device_scalar(void* stream, nl_bf16* x, int64_t rows, int64
  *   m = b1 m + (1-b1) g;  v = b2 v + (1-b2) g^2
  *   p = p - lr * ( (m / bc1) / (sqrt(v / bc2) + eps) + wd * p )
  * with bc1 = 1 - b1^t, bc2 = 1 - b2^t for update number t (1-based).
+ * b1 and b2 are doubles, as optax's are Python floats: b and 1 - b are each
+ * formed in double and rounded once to fp32 (1 - 0.999 is 0.001f, where fp32
+ * arithmetic on 0.999f would give 0.00099998713).
  * If p_bf16 != NULL the updated weight is also written there as bf16 (row
  * stride ld_bf16): the compute copy the next forward reads, so no separate
  * cast pass is needed (model.py:372-375 casts every parameter each step).
  */
 int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const float* g, float* m, float* v,
-                  nl_bf16* p_bf16, int64_t ld_bf16, float lr, float b1, float b2, float eps, float wd,
+                  nl_bf16* p_bf16, int64_t ld_bf16, float lr, double b1, double b2, float eps, float wd,
                   float bc1, float bc2);
 
 /* The same update over a whole parameter tree in ONE launch (the optax update
@@ -338,7 +341,7 @@ typedef struct nl_adamw_tensor {
 } nl_adamw_tensor;
 int64_t nl_adamw_multi_prepare(int n_tensors, nl_adamw_tensor* tensors_host);
 int nl_adamw_multi(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
-                   const float* hyper_dev, float b1, float b2, float eps, float wd);
+                   const float* hyper_dev, double b1, double b2, float eps, float wd);
 
 /* ======================================================================== */
 /* LayerNorm, bias gradients, embedding                                       */

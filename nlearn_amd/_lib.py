@@ -41,6 +41,7 @@ _P = ctypes.c_void_p
 _I = ctypes.c_int
 _I64 = ctypes.c_int64
 _F = ctypes.c_float
+_D = ctypes.c_double
 _S = AttnStride
 
 # name -> argtypes (restype is int unless listed in _RESTYPES)
@@ -71,9 +72,9 @@ _SIGNATURES = {
     "nl_lce_bwd_dlogits": [_P, _I, _I, _I, _I, _I, _P, _I64, _P, _I64, _P, _P, _F, _P, _P, _I64],
     "nl_mean_f32": [_P, _P, _I, _P],
     "nl_scale_bf16_by_device_scalar": [_P, _P, _I64, _I64, _I64, _P],
-    "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _F, _F, _F, _F, _F, _F],
+    "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _D, _D, _F, _F, _F, _F],
     "nl_adamw_multi_prepare": [_I, _P],
-    "nl_adamw_multi": [_P, _I, _P, _I64, _P, _F, _F, _F, _F],
+    "nl_adamw_multi": [_P, _I, _P, _I64, _P, _D, _D, _F, _F],
     "nl_layernorm_fwd": [_P, _I, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P],
     "nl_layernorm_bwd_ws_bytes": [_I, _I],
     "nl_layernorm_bwd": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t],

@@ -8,12 +8,23 @@
 namespace nl {
 namespace {
 
-// One element of the update. Every multiply-add is an explicit fmaf, so the
-// rounding is fixed by the source and all kernels below agree bit for bit.
-__device__ __forceinline__ void adam1(float gi, float& m, float& v, float& p, float lr, float b1, float b2, float eps,
+// The decay rates as the kernels use them: b and 1 - b, each rounded once to
+// fp32 from the caller's double (optax computes (1 - b) * g with b a Python
+// float: 1 - 0.999 in fp32 arithmetic would be 0.00099998713, not 0.001).
+struct Betas {
+  float b1, omb1, b2, omb2;
+};
+Betas make_betas(double b1, double b2) { return Betas{(float)b1, (float)(1.0 - b1), (float)b2, (float)(1.0 - b2)}; }
+
+// One element of the update, in optax.adamw's order (scale_by_adam, then
+// add_decayed_weights, then -lr): m = (1-b1) g + b1 m, v = (1-b2) g^2 + b2 v,
+// p -= lr * (m/bc1 / (sqrt(v/bc2) + eps) + wd p). Every multiply-add is an
+// explicit fmaf, so the rounding is fixed by the source and all kernels below
+// agree bit for bit.
+__device__ __forceinline__ void adam1(float gi, float& m, float& v, float& p, float lr, const Betas& bt, float eps,
                                       float wd, float inv_bc1, float inv_bc2) {
-  m = __builtin_fmaf(b1, m, (1.f - b1) * gi);
-  v = __builtin_fmaf(b2, v, ((1.f - b2) * gi) * gi);
+  m = __builtin_fmaf(bt.b1, m, bt.omb1 * gi);
+  v = __builtin_fmaf(bt.b2, v, bt.omb2 * (gi * gi));
   const float step = (m * inv_bc1) / (__builtin_sqrtf(v * inv_bc2) + eps);
   p = __builtin_fmaf(-lr, __builtin_fmaf(wd, p, step), p);
 }
@@ -21,14 +32,14 @@ __device__ __forceinline__ void adam1(float gi, float& m, float& v, float& p, fl
 __global__ __launch_bounds__(256) void adamw_kernel(int64_t rows, int64_t cols, float* __restrict__ p,
                                                     const float* __restrict__ g, float* __restrict__ m,
                                                     float* __restrict__ v, uint16_t* __restrict__ pb, int64_t ldb,
-                                                    float lr, float b1, float b2, float eps, float wd, float bc1,
+                                                    float lr, Betas bt, float eps, float wd, float bc1,
                                                     float bc2) {
   const float inv_bc1 = 1.f / bc1, inv_bc2 = 1.f / bc2;
   const int64_t n = rows * cols;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
     float mi = m[i], vi = v[i], pn = p[i];
-    adam1(g[i], mi, vi, pn, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+    adam1(g[i], mi, vi, pn, lr, bt, eps, wd, inv_bc1, inv_bc2);
     m[i] = mi;
     v[i] = vi;
     p[i] = pn;
@@ -43,8 +54,7 @@ __global__ __launch_bounds__(256) void adamw_kernel(int64_t rows, int64_t cols, 
 __global__ __launch_bounds__(256) void adamw_vec4_kernel(int64_t n4, f32x4* __restrict__ p,
                                                          const f32x4* __restrict__ g, f32x4* __restrict__ m,
                                                          f32x4* __restrict__ v, u32x2* __restrict__ pb, float lr,
-                                                         float b1, float b2, float eps, float wd, float bc1,
-                                                         float bc2) {
+                                                         Betas bt, float eps, float wd, float bc1, float bc2) {
   const float inv_bc1 = 1.f / bc1, inv_bc2 = 1.f / bc2;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
@@ -53,7 +63,7 @@ __global__ __launch_bounds__(256) void adamw_vec4_kernel(int64_t n4, f32x4* __re
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float a = mi[e], b = vi[e], c = pn[e];
-      adam1(gi[e], a, b, c, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+      adam1(gi[e], a, b, c, lr, bt, eps, wd, inv_bc1, inv_bc2);
       mi[e] = a, vi[e] = b, pn[e] = c;
     }
     m[i] = mi;
@@ -68,8 +78,8 @@ constexpr int kChunk = 8192;  // elements per workgroup of the multi-tensor upda
 // One workgroup per chunk of kChunk elements of one leaf; the leaf is found by
 // a binary search over chunk0 (the table is sorted by construction).
 __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_tensor* __restrict__ T,
-                                                          const float* __restrict__ hyper, float b1, float b2,
-                                                          float eps, float wd) {
+                                                          const float* __restrict__ hyper, Betas bt, float eps,
+                                                          float wd) {
   const int64_t chunk = blockIdx.x;
   int lo = 0, hi = n - 1;
   while (lo < hi) {
@@ -99,7 +109,7 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       float mk = m[k], vk = v[k], pk = p[k];
-      adam1(gi[k], mk, vk, pk, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+      adam1(gi[k], mk, vk, pk, lr, bt, eps, wd, inv_bc1, inv_bc2);
       m[k] = mk, v[k] = vk, p[k] = pk;
     }
     __builtin_nontemporal_store(m, reinterpret_cast<f32x4*>(t.m + e));
@@ -125,7 +135,7 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
   }
   for (e = v1 + threadIdx.x; e < e1; e += 256) {
     float m = t.m[e], v = t.v[e], p = t.p[e];
-    adam1(t.g[e], m, v, p, lr, b1, b2, eps, wd, inv_bc1, inv_bc2);
+    adam1(t.g[e], m, v, p, lr, bt, eps, wd, inv_bc1, inv_bc2);
     t.m[e] = m;
     t.v[e] = v;
     t.p[e] = p;
@@ -159,18 +169,18 @@ extern "C" int64_t nl_adamw_multi_prepare(int n_tensors, nl_adamw_tensor* T) {
 }
 
 extern "C" int nl_adamw_multi(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
-                              const float* hyper_dev, float b1, float b2, float eps, float wd) {
+                              const float* hyper_dev, double b1, double b2, float eps, float wd) {
   if (n_tensors < 0 || n_chunks < 0) return nl_set_error(NL_EINVAL, "adamw_multi: negative count");
   if (n_tensors == 0 || n_chunks == 0) return NL_OK;
   if (!tensors_dev || !hyper_dev) return nl_set_error(NL_EINVAL, "adamw_multi: null pointer");
   if (n_chunks > 0x7fffffff) return nl_set_error(NL_EINVAL, "adamw_multi: too many chunks");
   hipLaunchKernelGGL(adamw_multi_kernel, dim3((unsigned)n_chunks), dim3(256), 0, (hipStream_t)stream, n_tensors,
-                     tensors_dev, hyper_dev, b1, b2, eps, wd);
+                     tensors_dev, hyper_dev, make_betas(b1, b2), eps, wd);
   return nl_check_launch("nl_adamw_multi");
 }
 
 extern "C" int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const float* g, float* m, float* v,
-                             nl_bf16* p_bf16, int64_t ld_bf16, float lr, float b1, float b2, float eps, float wd,
+                             nl_bf16* p_bf16, int64_t ld_bf16, float lr, double b1, double b2, float eps, float wd,
                              float bc1, float bc2) {
   if (rows < 0 || cols < 0) return nl_set_error(NL_EINVAL, "adamw: negative size");
   if (rows == 0 || cols == 0) return NL_OK;
@@ -186,11 +196,12 @@ extern "C" int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p,
     const int64_t n4 = n / 4;
     const int64_t blocks = std::min<int64_t>((n4 + 255) / 256, 8192);
     hipLaunchKernelGGL(adamw_vec4_kernel, dim3((unsigned)blocks), dim3(256), 0, st, n4, (f32x4*)p,
-                       (const f32x4*)g, (f32x4*)m, (f32x4*)v, (u32x2*)p_bf16, lr, b1, b2, eps, wd, bc1, bc2);
+                       (const f32x4*)g, (f32x4*)m, (f32x4*)v, (u32x2*)p_bf16, lr, make_betas(b1, b2), eps, wd,
+                       bc1, bc2);
   } else {
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 8192);
     hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)blocks), dim3(256), 0, st, rows, cols, p, g, m, v, p_bf16,
-                       p_bf16 ? ld_bf16 : cols, lr, b1, b2, eps, wd, bc1, bc2);
+                       p_bf16 ? ld_bf16 : cols, lr, make_betas(b1, b2), eps, wd, bc1, bc2);
   }
   return nl_check_launch("nl_adamw_step");
 }
