@@ -22,7 +22,12 @@ def bf16_bits(x) -> np.ndarray:
     u = f.view(np.uint32)
     # finite values cannot overflow 32 bits here (largest is 0xFF7FFFFF + 0x8000);
     # NaN patterns are replaced below
-    r = ((u + (np.uint32(0x7FFF) + ((u >> 16) & np.uint32(1)))) >> 16).astype(np.uint16)
+    r = u >> 16                       # (u + 0x7FFF + lsb) >> 16, in place on one temporary
+    r &= np.uint32(1)
+    r += np.uint32(0x7FFF)
+    r += u
+    r >>= 16
+    r = r.astype(np.uint16)
     nan = np.isnan(f)
     if nan.any():
         r = np.where(nan, ((u >> 16) | np.uint32(0x40)).astype(np.uint16), r)

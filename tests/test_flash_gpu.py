@@ -180,3 +180,25 @@ def test_flash_baseline_shapes(dev, n, S):
     sdk = dk.float().sum(2)
     assert (sdk.norm() / (dk.float().norm() * math.sqrt(S))).item() < 2e-2
     assert torch.isfinite(O.float()).all() and torch.isfinite(dq.float()).all()
+
+
+@pytest.mark.parametrize("name", ["flash_s1_2x128x64", "flash_s2_2x128x64"])
+def test_flash_preprocess_D_golden(dev, name):
+    """D = rowsum(dO * O) (attention.py:116), the preprocess kernel, against the
+    golden D computed by the float64 oracle from the same O and dO."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.attention import _stride4
+
+    g = np.load(GOLDEN / f"{name}.npz")
+    O = _dev_bf16(ops.bf16_bits(g["O"].astype(np.float32)), dev)[:, None]
+    dO = _dev_bf16(g["dO"], dev)[:, None]
+    B, H, S, Dh = O.shape
+    D = torch.full((B, H, S), float("nan"), dtype=torch.float32, device=dev)
+    _lib.call("nl_flash_attention_bwd_preprocess", torch.cuda.current_stream(dev).cuda_stream, B, H, S, Dh,
+              O.data_ptr(), _stride4(O), dO.data_ptr(), _stride4(dO), D.data_ptr())
+    torch.cuda.synchronize()
+    # the golden D uses the float64 O; the kernel reads O rounded to bf16
+    ref = (ops.bf16_round(g["O"].astype(np.float32)).astype(np.float64) * ops.bf16_to_f32(g["dO"])).sum(-1)
+    assert np.abs(_np(D)[:, 0] - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+    assert rel_l2(_np(D)[:, 0], g["D"]) <= TOL

@@ -1,0 +1,96 @@
+"""Training-step parity at BASELINE's own configurations, against the NumPy oracle.
+
+* configs[4], the metric's configuration (bs32 x seq512, the step bench.py
+  times): the first step's loss and every parameter gradient, with the
+  weight-gradient stream and the deferred LayerNorm sums on (as in the bench),
+  then two more steps through the captured HIP graph; through both loss paths
+  (LM head + CE, and linear_cross_entropy). Constant lr 1e-3 (the peak lr).
+* configs[0] with BASELINE.md's parity companion: bs4 x seq512, AdamW lr 3e-4,
+  a 20-step loss curve through the HIP graph from the same initial weights
+  and batches as the oracle.
+
+Tolerances (north_star): loss within 1e-2 at every step; gradients rel-L2 <
+5e-2 (the device computes in bf16 with fp32 accumulation, the oracle in fp32
+with bf16-rounded operands).
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+from oracle import model_np as om
+
+pytestmark = pytest.mark.gpu
+
+LR32 = 1e-3
+NAMES = ["tok", "pos"] + [f"b{i}.{n}" for i in range(4) for n in
+                          ("ln1.g", "ln1.b", "Wqkv", "Wo", "ln2.g", "ln2.b", "W1", "b1", "W2", "b2")] + \
+        ["lnf.g", "lnf.b", "head"]
+
+
+@pytest.fixture(scope="module")
+def bs32_oracle():
+    """Three oracle steps at bs32 x seq512: losses, and step 1's gradients."""
+    rng = np.random.default_rng(3232)
+    batches = [rng.integers(0, 50257, (32, 513)).astype(np.int32) for _ in range(3)]
+    params = om.init_params(0)
+    opt = om.AdamWNP(params, lambda c: LR32)
+    print("oracle bs32 step 1", flush=True)
+    loss1, g1 = om.loss_and_grads(params, batches[0].astype(np.int64))
+    opt.step(params, g1)
+    print("oracle bs32 step 2", flush=True)
+    loss2, g2 = om.loss_and_grads(params, batches[1].astype(np.int64))
+    opt.step(params, g2)
+    del g2
+    print("oracle bs32 step 3 (forward)", flush=True)
+    loss3, _ = om.loss_and_grads(params, batches[2].astype(np.int64), grads=False)
+    return batches, [loss1, loss2, loss3], g1
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("fused", [False, True], ids=["linear+ce", "linear_cross_entropy"])
+def test_metric_config_bs32_step_matches_oracle(dev, bs32_oracle, fused):
+    import torch
+    from nlearn_amd.model import init_model, tree_leaves
+    from nlearn_amd.train import AdamW, make_train_step
+
+    batches, ref_losses, g1 = bs32_oracle
+    opt = AdamW(lambda c: LR32)
+    params = init_model(0, device=dev)
+    state = opt.init(params)
+    step = make_train_step(opt, graph=True, warmup=1, fused_lmhead=fused)
+    got = []
+    for i, b in enumerate(batches):
+        print(f"device bs32 step {i + 1} fused={fused}", flush=True)
+        params, state, loss = step(params, state, torch.from_numpy(b).to(dev))
+        got.append(loss.item())
+        if i == 0:  # the eager step: main_grad now holds step 1's gradients
+            for name, p, g in zip(NAMES, tree_leaves(params), om._leaves(g1)):
+                err = rel_l2(p.main_grad.float().cpu().numpy(), g, floor=1e-8)
+                assert err < 5e-2, (name, err)
+    print("device", np.round(got, 5).tolist(), "oracle", np.round(ref_losses, 5).tolist())
+    assert np.abs(np.array(got) - np.array(ref_losses)).max() < 1e-2
+
+
+@pytest.mark.timeout(900)
+def test_configs0_bs4_20_step_curve_matches_oracle(dev):
+    import torch
+    from nlearn_amd.model import init_model
+    from nlearn_amd.train import AdamW, make_train_step
+
+    rng = np.random.default_rng(404)
+    batches = [rng.integers(0, 50257, (4, 513)).astype(np.int32) for _ in range(20)]
+    opt = AdamW(lambda c: 3e-4)
+    params = init_model(0, device=dev)
+    state = opt.init(params)
+    step = make_train_step(opt, graph=True)
+    gpu = []
+    for b in batches:
+        params, state, loss = step(params, state, torch.from_numpy(b).to(dev))
+        gpu.append(loss.item())
+    ref = om.TrainStepNP(om.init_params(0), lr=3e-4, warmup=0, decay_steps=0)
+    cpu = []
+    for i, b in enumerate(batches):
+        cpu.append(ref(b.astype(np.int64)))
+        print(f"oracle bs4 step {i + 1}: {cpu[-1]:.5f} (device {gpu[i]:.5f})", flush=True)
+    diff = np.abs(np.array(gpu) - np.array(cpu))
+    assert diff.max() < 1e-2, diff.tolist()
