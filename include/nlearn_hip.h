@@ -343,6 +343,35 @@ int64_t nl_adamw_multi_prepare(int n_tensors, nl_adamw_tensor* tensors_host);
 int nl_adamw_multi(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
                    const float* hyper_dev, double b1, double b2, float eps, float wd);
 
+/* nl_adamw_multi with optax.clip_by_global_norm(max_norm) chained in front of
+ * it (train.py:502-506: optax.chain(clip_by_global_norm(NLEARN_GRAD_CLIP),
+ * adamw)): every gradient element is used as g while *gnorm_dev < max_norm,
+ * else as (g / *gnorm_dev) * max_norm. *gnorm_dev is the global L2 norm over
+ * all leaves, e.g. written by nl_global_norm on the same stream. */
+int nl_adamw_multi_clip(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
+                        const float* hyper_dev, double b1, double b2, float eps, float wd,
+                        const float* gnorm_dev, float max_norm);
+
+/* out[0] = sqrt(sum_i g[i]^2) over a dense fp32 vector (16-byte aligned; the
+ * model's whole gradient buffer, whose padding is zero): optax.global_norm as
+ * clip_by_global_norm uses it. Fixed summation order (bitwise reproducible);
+ * workspace of nl_global_norm_ws_bytes(n) bytes. Two launches, no host sync. */
+size_t nl_global_norm_ws_bytes(int64_t n);
+int nl_global_norm(void* stream, int64_t n, const float* g, float* out, void* ws, size_t ws_bytes);
+
+/* Gradient accumulation over micro-steps, as optax.MultiSteps does it
+ * (train.py:319-325,507-508 wrap the optimizer in MultiSteps(every_k_schedule=
+ * NLEARN_GRAD_ACCUM)), with the loss-scale division of train_step
+ * (train.py:332-337, g / NLEARN_LOSS_SCALE) in front:
+ *   u = g[i] / coef_dev[0];
+ *   acc[i] = u                                   if coef_dev[1] == 1,
+ *          = acc[i] + (u - acc[i]) / coef_dev[1]  otherwise,
+ * with coef_dev[1] = (micro-step index) + 1: acc is the running mean of the
+ * micro-steps' gradients. Both scalars are read on the device (a captured
+ * graph replays with the values written before each replay). acc may equal g
+ * (unscaling in place). n elements, 16-byte aligned. */
+int nl_grad_accumulate(void* stream, int64_t n, float* acc, const float* g, const float* coef_dev);
+
 /* ======================================================================== */
 /* LayerNorm, bias gradients, embedding                                       */
 /* ======================================================================== */

@@ -75,6 +75,10 @@ _SIGNATURES = {
     "nl_adamw_step": [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _F, _D, _D, _F, _F, _F, _F],
     "nl_adamw_multi_prepare": [_I, _P],
     "nl_adamw_multi": [_P, _I, _P, _I64, _P, _D, _D, _F, _F],
+    "nl_adamw_multi_clip": [_P, _I, _P, _I64, _P, _D, _D, _F, _F, _P, _F],
+    "nl_global_norm_ws_bytes": [_I64],
+    "nl_global_norm": [_P, _I64, _P, _P, _P, ctypes.c_size_t],
+    "nl_grad_accumulate": [_P, _I64, _P, _P, _P],
     "nl_layernorm_fwd": [_P, _I, _I, _P, _P, _P, _P, _P, _F, _P, _P, _P],
     "nl_layernorm_bwd_ws_bytes": [_I, _I],
     "nl_layernorm_bwd": [_P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, ctypes.c_size_t],
@@ -96,6 +100,7 @@ _RESTYPES = {
     "nl_adamw_multi_prepare": ctypes.c_int64,
     "nl_colsum_ws_bytes": ctypes.c_size_t,
     "nl_lce_ws_bytes": ctypes.c_size_t,
+    "nl_global_norm_ws_bytes": ctypes.c_size_t,
 }
 
 EXPORTED = tuple(_SIGNATURES)

@@ -105,10 +105,11 @@ def _resume_path(run_name) -> str:
 
 def save_resume_state(params, opt_state: dict, step: int, run_name=None) -> str:
     """Parameters, AdamW state and the next step, atomically (train.py:76-89)."""
-    state = {"params": to_numpy(params),
-             "opt_state": {"count": int(opt_state["count"]), "mu": to_numpy(opt_state["mu"]),
-                           "nu": to_numpy(opt_state["nu"])},
-             "step": int(step)}
+    so = {"count": int(opt_state["count"]), "mu": to_numpy(opt_state["mu"]), "nu": to_numpy(opt_state["nu"])}
+    if "mini_step" in opt_state:  # MultiSteps: the micro-step and the running mean so far
+        so["mini_step"] = int(opt_state["mini_step"])
+        so["acc"] = to_numpy(opt_state["acc_flat"])
+    state = {"params": to_numpy(params), "opt_state": so, "step": int(step)}
     path = _resume_path(run_name)
     _atomic_dump(state, path)
     return path
@@ -136,4 +137,13 @@ def load_resume_state(optimizer, run_name=None, device="cuda"):
                 raise ValueError(f"resume: moment shape {np.shape(src)} != {tuple(dst.shape)}")
             dst.copy_(torch.from_numpy(np.asarray(src, np.float32)))
     state["count"] = int(so["count"])
+    if "inner" in state:  # MultiSteps around AdamW
+        state["inner"]["count"] = int(so["count"])
+        if "mini_step" in so:
+            acc = np.asarray(so["acc"], np.float32)
+            if acc.shape != tuple(state["acc_flat"].shape):
+                raise ValueError("resume: the accumulated gradient does not match the parameter tree")
+            state["mini_step"] = int(so["mini_step"])
+            with torch.no_grad():
+                state["acc_flat"].copy_(torch.from_numpy(acc))
     return params, state, int(saved["step"])

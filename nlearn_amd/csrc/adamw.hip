@@ -77,9 +77,11 @@ constexpr int kChunk = 8192;  // elements per workgroup of the multi-tensor upda
 
 // One workgroup per chunk of kChunk elements of one leaf; the leaf is found by
 // a binary search over chunk0 (the table is sorted by construction).
+template <bool CLIP>
 __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_tensor* __restrict__ T,
                                                           const float* __restrict__ hyper, Betas bt, float eps,
-                                                          float wd) {
+                                                          float wd, const float* __restrict__ gnorm_dev,
+                                                          float max_norm) {
   const int64_t chunk = blockIdx.x;
   int lo = 0, hi = n - 1;
   while (lo < hi) {
@@ -89,6 +91,10 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
   }
   const nl_adamw_tensor t = T[lo];
   const float lr = hyper[0], inv_bc1 = 1.f / hyper[1], inv_bc2 = 1.f / hyper[2];
+  // optax.clip_by_global_norm: g unchanged while ||g|| < max_norm, else (g / ||g||) * max_norm
+  const float gnorm = CLIP ? *gnorm_dev : 0.f;
+  const bool clip = CLIP && !(gnorm < max_norm);
+  auto clipped = [&](float g) { return clip ? (g / gnorm) * max_norm : g; };
   const int64_t numel = t.rows * t.cols;
   const int64_t e0 = (chunk - t.chunk0) * kChunk;
   const int64_t e1 = min(numel, e0 + kChunk);
@@ -109,7 +115,7 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       float mk = m[k], vk = v[k], pk = p[k];
-      adam1(gi[k], mk, vk, pk, lr, bt, eps, wd, inv_bc1, inv_bc2);
+      adam1(clipped(gi[k]), mk, vk, pk, lr, bt, eps, wd, inv_bc1, inv_bc2);
       m[k] = mk, v[k] = vk, p[k] = pk;
     }
     __builtin_nontemporal_store(m, reinterpret_cast<f32x4*>(t.m + e));
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
   }
   for (e = v1 + threadIdx.x; e < e1; e += 256) {
     float m = t.m[e], v = t.v[e], p = t.p[e];
-    adam1(t.g[e], m, v, p, lr, bt, eps, wd, inv_bc1, inv_bc2);
+    adam1(clipped(t.g[e]), m, v, p, lr, bt, eps, wd, inv_bc1, inv_bc2);
     t.m[e] = m;
     t.v[e] = v;
     t.p[e] = p;
@@ -146,10 +152,106 @@ __global__ __launch_bounds__(256) void adamw_multi_kernel(int n, const nl_adamw_
   }
 }
 
+// optax.MultiSteps's running mean of micro-step gradients, with the loss-scale
+// division of the reference's train_step in front of it:
+//   u = g / coef[0];  acc = (coef[1] == 1) ? u : acc + (u - acc) / coef[1]
+// (coef[1] = mini_step + 1; optax's acc is zero on the first micro-step, so
+// its formula reduces to acc = u there). acc may equal g (in-place unscale).
+__global__ __launch_bounds__(256) void grad_accumulate_kernel(int64_t n, float* acc, const float* g,
+                                                              const float* __restrict__ coef) {
+  const float s = coef[0], k1 = coef[1];
+  const bool first = k1 == 1.f;
+  const int64_t n4 = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const f32x4 gi = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g) + i);
+    f32x4 a = first ? f32x4{0.f, 0.f, 0.f, 0.f} : reinterpret_cast<const f32x4*>(acc)[i];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float u = gi[k] / s;
+      a[k] = first ? u : a[k] + (u - a[k]) / k1;
+    }
+    reinterpret_cast<f32x4*>(acc)[i] = a;
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+    const float u = g[i] / s;
+    acc[i] = first ? u : acc[i] + (u - acc[i]) / k1;
+  }
+}
+
+constexpr int kNormParts = 1024;  // partial sums of the global norm (fixed, so the order is fixed)
+
+__device__ __forceinline__ float block_sum256(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// part[b] = sum of g[i]^2 over the elements block b visits (grid-stride, fixed order)
+__global__ __launch_bounds__(256) void sumsq_partial_kernel(int64_t n, const float* __restrict__ g,
+                                                            float* __restrict__ part) {
+  __shared__ float red[4];
+  float acc = 0.f;
+  const int64_t n4 = n / 4;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride) {
+    const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(g) + i);
+    acc = __builtin_fmaf(x[0], x[0], acc);
+    acc = __builtin_fmaf(x[1], x[1], acc);
+    acc = __builtin_fmaf(x[2], x[2], acc);
+    acc = __builtin_fmaf(x[3], x[3], acc);
+  }
+  for (int64_t i = n4 * 4 + (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+    acc = __builtin_fmaf(g[i], g[i], acc);
+  const float t = block_sum256(acc, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = t;
+}
+
+// out[0] = sqrt(sum of the partials), reduced in a fixed order
+__global__ __launch_bounds__(256) void sumsq_final_kernel(int parts, const float* __restrict__ part,
+                                                          float* __restrict__ out) {
+  __shared__ float red[4];
+  float acc = 0.f;
+  for (int i = threadIdx.x; i < parts; i += 256) acc += part[i];
+  const float t = block_sum256(acc, red);
+  if (threadIdx.x == 0) out[0] = __builtin_sqrtf(t);
+}
+
 }  // namespace
 }  // namespace nl
 
 using namespace nl;
+
+extern "C" int nl_grad_accumulate(void* stream, int64_t n, float* acc, const float* g, const float* coef_dev) {
+  if (n < 0) return nl_set_error(NL_EINVAL, "grad_accumulate: negative size");
+  if (n == 0) return NL_OK;
+  if (!acc || !g || !coef_dev) return nl_set_error(NL_EINVAL, "grad_accumulate: null pointer");
+  if ((((uintptr_t)acc | (uintptr_t)g) & 15) != 0)
+    return nl_set_error(NL_EALIGN, "grad_accumulate: acc and g must be 16-byte aligned");
+  const int64_t blocks = std::min<int64_t>((n / 4 + 255) / 256 + 1, 8192);
+  hipLaunchKernelGGL(grad_accumulate_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream, n, acc, g,
+                     coef_dev);
+  return nl_check_launch("nl_grad_accumulate");
+}
+
+extern "C" size_t nl_global_norm_ws_bytes(int64_t n) { return n > 0 ? kNormParts * sizeof(float) : 0; }
+
+extern "C" int nl_global_norm(void* stream, int64_t n, const float* g, float* out, void* ws, size_t ws_bytes) {
+  if (n < 0) return nl_set_error(NL_EINVAL, "global_norm: negative size");
+  if (!out) return nl_set_error(NL_EINVAL, "global_norm: null output");
+  if (n > 0 && (!g || !ws)) return nl_set_error(NL_EINVAL, "global_norm: null pointer");
+  if (n > 0 && ws_bytes < nl_global_norm_ws_bytes(n))
+    return nl_set_error(NL_EINVAL, "global_norm: workspace smaller than nl_global_norm_ws_bytes()");
+  if (((uintptr_t)g & 15) != 0) return nl_set_error(NL_EALIGN, "global_norm: g must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  float* part = static_cast<float*>(ws);
+  if (n > 0)
+    hipLaunchKernelGGL(sumsq_partial_kernel, dim3(kNormParts), dim3(256), 0, st, n, g, part);
+  hipLaunchKernelGGL(sumsq_final_kernel, dim3(1), dim3(256), 0, st, n > 0 ? kNormParts : 0, part, out);
+  return nl_check_launch("nl_global_norm");
+}
 
 extern "C" int64_t nl_adamw_multi_prepare(int n_tensors, nl_adamw_tensor* T) {
   if (n_tensors < 0 || (n_tensors > 0 && !T)) return -(int64_t)nl_set_error(NL_EINVAL, "adamw_multi: bad table");
@@ -174,9 +276,22 @@ extern "C" int nl_adamw_multi(void* stream, int n_tensors, const nl_adamw_tensor
   if (n_tensors == 0 || n_chunks == 0) return NL_OK;
   if (!tensors_dev || !hyper_dev) return nl_set_error(NL_EINVAL, "adamw_multi: null pointer");
   if (n_chunks > 0x7fffffff) return nl_set_error(NL_EINVAL, "adamw_multi: too many chunks");
-  hipLaunchKernelGGL(adamw_multi_kernel, dim3((unsigned)n_chunks), dim3(256), 0, (hipStream_t)stream, n_tensors,
-                     tensors_dev, hyper_dev, make_betas(b1, b2), eps, wd);
+  hipLaunchKernelGGL(adamw_multi_kernel<false>, dim3((unsigned)n_chunks), dim3(256), 0, (hipStream_t)stream,
+                     n_tensors, tensors_dev, hyper_dev, make_betas(b1, b2), eps, wd, nullptr, 0.f);
   return nl_check_launch("nl_adamw_multi");
+}
+
+extern "C" int nl_adamw_multi_clip(void* stream, int n_tensors, const nl_adamw_tensor* tensors_dev, int64_t n_chunks,
+                                   const float* hyper_dev, double b1, double b2, float eps, float wd,
+                                   const float* gnorm_dev, float max_norm) {
+  if (n_tensors < 0 || n_chunks < 0) return nl_set_error(NL_EINVAL, "adamw_multi: negative count");
+  if (!(max_norm > 0.f)) return nl_set_error(NL_EINVAL, "adamw_multi_clip: max_norm must be > 0");
+  if (n_tensors == 0 || n_chunks == 0) return NL_OK;
+  if (!tensors_dev || !hyper_dev || !gnorm_dev) return nl_set_error(NL_EINVAL, "adamw_multi: null pointer");
+  if (n_chunks > 0x7fffffff) return nl_set_error(NL_EINVAL, "adamw_multi: too many chunks");
+  hipLaunchKernelGGL(adamw_multi_kernel<true>, dim3((unsigned)n_chunks), dim3(256), 0, (hipStream_t)stream,
+                     n_tensors, tensors_dev, hyper_dev, make_betas(b1, b2), eps, wd, gnorm_dev, max_norm);
+  return nl_check_launch("nl_adamw_multi_clip");
 }
 
 extern "C" int nl_adamw_step(void* stream, int64_t rows, int64_t cols, float* p, const float* g, float* m, float* v,

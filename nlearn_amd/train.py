@@ -4,8 +4,14 @@
                                      (train.py:270-299, the batched fused-CE path)
 * ``warmup_cosine_decay_schedule``   optax's schedule (train.py:487-495)
 * ``AdamW``                          optax.adamw semantics (train.py:504-505) on the
-                                     fused HIP kernel; writes the bf16 weight shadows
-* ``make_train_step(optimizer)``     value_and_grad + update (train.py:328-341)
+                                     fused HIP kernel; writes the bf16 weight shadows;
+                                     ``clip_norm`` chains optax.clip_by_global_norm
+                                     in front (NLEARN_GRAD_CLIP, train.py:502-506)
+* ``MultiSteps``                     optax.MultiSteps gradient accumulation
+                                     (NLEARN_GRAD_ACCUM, train.py:319-325,507-508)
+* ``make_train_step(optimizer)``     value_and_grad + update (train.py:328-341), with
+                                     the static loss scale (NLEARN_LOSS_SCALE,
+                                     train.py:313-316,332-337)
 * ``train(...)``                     offline loop on a synthetic uniform token stream
                                      (train.py:482-622 streams a HF corpus instead),
                                      with the reference's checkpoint / resume files
@@ -37,6 +43,11 @@ CHECKPOINT_EVERY = int(os.environ.get("NLEARN_CHECKPOINT_EVERY", "1000"))
 PEAK_LR = 1e-3
 WEIGHT_DECAY = float(os.environ.get("NLEARN_WD", "0.1"))
 BATCH_SIZE = 32
+# train.py:313-325,502: static loss scale (1 = off), micro-batches per update,
+# global-norm clipping threshold (0 = off)
+LOSS_SCALE = float(os.environ.get("NLEARN_LOSS_SCALE", "1.0"))
+GRAD_ACCUM = int(os.environ.get("NLEARN_GRAD_ACCUM", "1"))
+GRAD_CLIP = float(os.environ.get("NLEARN_GRAD_CLIP", "0"))
 
 
 # ---------------------------------------------------------------------------
@@ -128,44 +139,72 @@ def attach_grad_buffers(params) -> torch.Tensor:
     return flat
 
 
+def _pinned_to(dst: torch.Tensor, values) -> None:
+    """Stream-ordered copy of host scalars into a device tensor (freshly pinned
+    memory, so an earlier copy still in flight is never overwritten)."""
+    dst.copy_(torch.tensor(values, dtype=torch.float32).pin_memory(), non_blocking=True)
+
+
+def _same_layout_view(flat: torch.Tensor, like: torch.Tensor, like_flat: torch.Tensor) -> torch.Tensor:
+    """The view of ``flat`` at the position and with the strides ``like`` has in ``like_flat``."""
+    return torch.as_strided(flat, like.shape, like.stride(), like.storage_offset() - like_flat.storage_offset())
+
+
 class AdamW:
     """optax.adamw(learning_rate=schedule, b1=.9, b2=.999, eps=1e-8, weight_decay)
     with decoupled decay on every parameter. The schedule is evaluated at the
     update count before the update (optax's ``count``), bias corrections use the
-    count after it.
+    count after it. ``clip_norm`` > 0 puts optax.clip_by_global_norm(clip_norm)
+    in front (train.py:502-506): the global norm is computed on the device and
+    read there by the update, so no host synchronisation is involved.
 
     ``init`` attaches fixed gradient buffers to the leaves (``main_grad``); the
     update is then ONE multi-tensor launch that reads lr and the bias
     corrections from device memory (``state["hyper"]``), so it can live inside
-    a captured HIP graph. ``prepare`` writes those scalars for the coming
-    update, ``apply`` launches it, ``update`` does both and counts the step.
-    Leaves without a buffer fall back to one launch per leaf on ``.grad``."""
+    a captured HIP graph. The step protocol, shared with ``MultiSteps``:
+    ``prepare`` writes the device scalars for the coming step, ``apply`` launches
+    the capturable work, ``finish`` runs what follows it outside a graph (nothing
+    here), ``advance`` counts the step; ``update`` does all four. Leaves without
+    a buffer fall back to one launch per leaf on ``.grad`` (no clipping there)."""
 
     def __init__(self, learning_rate, weight_decay: float = WEIGHT_DECAY, b1: float = 0.9, b2: float = 0.999,
-                 eps: float = 1e-8, grad_buffers: bool = True):
+                 eps: float = 1e-8, grad_buffers: bool = True, clip_norm: float = 0.0):
         self.lr = learning_rate if callable(learning_rate) else (lambda _c, v=learning_rate: v)
         self.wd, self.b1, self.b2, self.eps = weight_decay, b1, b2, eps
         self.grad_buffers = grad_buffers
+        self.clip_norm = float(clip_norm)
 
     def init(self, params) -> dict:
         leaves = tree_leaves(params)
+        dev = leaves[0].device
         flat = attach_grad_buffers(params) if self.grad_buffers else None
-        return {"count": 0,
-                "mu": [_zeros_with_layout(p) for p in leaves],
-                "nu": [_zeros_with_layout(p) for p in leaves],
-                "grad_flat": flat,
-                "hyper": torch.ones(3, dtype=torch.float32, device=leaves[0].device),
-                "table": None}
+        state = {"count": 0,
+                 "mu": [_zeros_with_layout(p) for p in leaves],
+                 "nu": [_zeros_with_layout(p) for p in leaves],
+                 "grad_flat": flat,
+                 # the gradients the update reads: main_grad (None) or views of grad_src_flat
+                 "grads": None, "grad_src_flat": flat,
+                 "hyper": torch.ones(3, dtype=torch.float32, device=dev),
+                 "unscale": torch.ones(2, dtype=torch.float32, device=dev), "unscale_value": 1.0,
+                 "table": None}
+        if self.clip_norm > 0 and flat is not None:
+            state["gnorm"] = torch.zeros(1, dtype=torch.float32, device=dev)
+            n = flat.numel()
+            state["norm_ws"] = torch.empty(max(int(_lib.load().nl_global_norm_ws_bytes(n)), 16) // 4,
+                                           dtype=torch.float32, device=dev)
+        return state
 
     def hyper_values(self, count: int):
         t = count + 1
         return float(self.lr(count)), 1.0 - self.b1 ** t, 1.0 - self.b2 ** t
 
-    def prepare(self, state: dict) -> None:
+    def prepare(self, state: dict, loss_scale: float = 1.0) -> None:
         """Write {lr, bc1, bc2} of update ``state["count"] + 1`` to the device
-        (an async copy from freshly pinned memory, ordered on the stream)."""
-        h = torch.tensor(self.hyper_values(state["count"]), dtype=torch.float32).pin_memory()
-        state["hyper"].copy_(h, non_blocking=True)
+        (and the loss-scale divisor, when it changed)."""
+        _pinned_to(state["hyper"], self.hyper_values(state["count"]))
+        if loss_scale != state["unscale_value"]:
+            _pinned_to(state["unscale"], (float(loss_scale), 1.0))
+            state["unscale_value"] = float(loss_scale)
 
     def _table(self, params, state):
         """Device table of the multi-tensor update, rebuilt when a bf16 shadow changed."""
@@ -180,10 +219,10 @@ class AdamW:
             return cached
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("AdamW: parameter layout changed during graph capture")
+        grads = state["grads"] or [p.main_grad for p in leaves]
         T = (_lib.AdamWTensor * len(leaves))()
-        for i, (p, m, v, sh) in enumerate(zip(leaves, state["mu"], state["nu"], shadows)):
+        for i, (p, g, m, v, sh) in enumerate(zip(leaves, grads, state["mu"], state["nu"], shadows)):
             rows, ld = _rows_ld(p)
-            g = p.main_grad
             if _rows_ld(g) != (rows, ld) or _rows_ld(m) != (rows, ld):
                 raise RuntimeError("AdamW: gradient / moment layout differs from the parameter's")
             T[i].p, T[i].g, T[i].m, T[i].v = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()
@@ -197,16 +236,31 @@ class AdamW:
         state["table"] = (key, dev_table, len(leaves), n_chunks)
         return state["table"]
 
-    def apply(self, params, state: dict) -> None:
-        """Launch the update with the scalars already on the device (no host sync)."""
+    def apply(self, params, state: dict, loss_scale: float = 1.0) -> None:
+        """Launch the update with the scalars already on the device (no host sync):
+        gradients / loss_scale (in place), the global norm if clipping, AdamW."""
         wgrad.join()  # gradients forked onto the weight-gradient stream must be complete
         leaves = tree_leaves(params)
         stream = torch.cuda.current_stream(leaves[0].device).cuda_stream
-        if all(getattr(p, "main_grad", None) is not None for p in leaves):
+        if state["grads"] is not None or all(getattr(p, "main_grad", None) is not None for p in leaves):
+            src = state["grad_src_flat"]
+            if loss_scale != 1.0:
+                # train.py:335-336 divides the gradients by the loss scale before the update
+                _lib.call("nl_grad_accumulate", stream, src.numel(), src.data_ptr(), src.data_ptr(),
+                          state["unscale"].data_ptr())
             _, table, n, n_chunks = self._table(params, state)
-            _lib.call("nl_adamw_multi", stream, n, table.data_ptr(), n_chunks, state["hyper"].data_ptr(),
-                      self.b1, self.b2, self.eps, self.wd)
+            if self.clip_norm > 0:
+                ws = state["norm_ws"]
+                _lib.call("nl_global_norm", stream, src.numel(), src.data_ptr(), state["gnorm"].data_ptr(),
+                          ws.data_ptr(), ws.numel() * 4)
+                _lib.call("nl_adamw_multi_clip", stream, n, table.data_ptr(), n_chunks, state["hyper"].data_ptr(),
+                          self.b1, self.b2, self.eps, self.wd, state["gnorm"].data_ptr(), self.clip_norm)
+            else:
+                _lib.call("nl_adamw_multi", stream, n, table.data_ptr(), n_chunks, state["hyper"].data_ptr(),
+                          self.b1, self.b2, self.eps, self.wd)
             return
+        if self.clip_norm > 0 or loss_scale != 1.0:
+            raise RuntimeError("AdamW: clipping and loss scaling need the gradient buffers (grad_buffers=True)")
         lr, bc1, bc2 = self.hyper_values(state["count"])
         for p, m, v in zip(leaves, state["mu"], state["nu"]):
             g = getattr(p, "main_grad", None)
@@ -225,25 +279,103 @@ class AdamW:
             _lib.call("nl_adamw_step", stream, rows, ld, p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(),
                       sb, ldb, lr, self.b1, self.b2, self.eps, self.wd, bc1, bc2)
 
-    def update(self, params, state: dict) -> dict:
-        """Apply one step in place (gradients from ``main_grad`` or ``.grad``)."""
-        self.prepare(state)
-        self.apply(params, state)
+    def finish(self, params, state: dict) -> None:
+        """Nothing runs after the captured part of an AdamW step."""
+
+    def advance(self, state: dict) -> None:
         state["count"] += 1
+
+    def update(self, params, state: dict, loss_scale: float = 1.0) -> dict:
+        """Apply one step in place (gradients from ``main_grad`` or ``.grad``)."""
+        self.prepare(state, loss_scale)
+        self.apply(params, state, loss_scale)
+        self.finish(params, state)
+        self.advance(state)
         return state
 
 
-def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool = False, warmup: int = 2,
-                    overlap_wgrad: bool = True, fused_lmhead: bool | None = None):
+class MultiSteps:
+    """optax.MultiSteps(inner, every_k_schedule=k) (train.py:319-325,507-508).
+
+    Every call is one micro-step. Its gradients (divided by the loss scale)
+    join the running mean acc + (g - acc) / (i + 1) of the micro-steps so far
+    (optax's formula, one HBM pass: ``nl_grad_accumulate``); every k-th call
+    then runs the inner optimizer (clipping and AdamW) on that mean and starts
+    over, and the parameters do not change on the other calls. The inner
+    count, and with it the schedule, advances once per k micro-steps. The
+    per-micro-step work is capturable; the inner update of the k-th call runs
+    after the captured part (``finish``), reading the same fixed buffers."""
+
+    def __init__(self, inner: AdamW, every_k: int):
+        if every_k < 1:
+            raise ValueError("MultiSteps: every_k must be >= 1")
+        if not inner.grad_buffers:
+            raise ValueError("MultiSteps: the inner optimizer needs gradient buffers")
+        self.inner, self.k = inner, int(every_k)
+
+    def init(self, params) -> dict:
+        inner = self.inner.init(params)
+        flat = inner["grad_flat"]
+        acc = torch.zeros_like(flat)
+        inner["grads"] = [_same_layout_view(acc, p.main_grad, flat) for p in tree_leaves(params)]
+        inner["grad_src_flat"] = acc
+        return {"inner": inner, "count": inner["count"], "mini_step": 0, "acc_flat": acc,
+                "coef": torch.ones(2, dtype=torch.float32, device=flat.device),
+                "mu": inner["mu"], "nu": inner["nu"]}
+
+    def _final(self, state) -> bool:
+        return state["mini_step"] + 1 == self.k
+
+    def prepare(self, state: dict, loss_scale: float = 1.0) -> None:
+        _pinned_to(state["coef"], (float(loss_scale), float(state["mini_step"] + 1)))
+        if self._final(state):
+            self.inner.prepare(state["inner"])
+
+    def apply(self, params, state: dict, loss_scale: float = 1.0) -> None:
+        wgrad.join()
+        stream = torch.cuda.current_stream(state["acc_flat"].device).cuda_stream
+        src = state["inner"]["grad_flat"]
+        _lib.call("nl_grad_accumulate", stream, src.numel(), state["acc_flat"].data_ptr(), src.data_ptr(),
+                  state["coef"].data_ptr())
+
+    def finish(self, params, state: dict) -> None:
+        if self._final(state):
+            self.inner.apply(params, state["inner"])
+
+    def advance(self, state: dict) -> None:
+        if self._final(state):
+            self.inner.advance(state["inner"])
+            state["mini_step"] = 0
+        else:
+            state["mini_step"] += 1
+        state["count"] = state["inner"]["count"]
+
+    def update(self, params, state: dict, loss_scale: float = 1.0) -> dict:
+        self.prepare(state, loss_scale)
+        self.apply(params, state, loss_scale)
+        self.finish(params, state)
+        self.advance(state)
+        return state
+
+
+def make_train_step(optimizer, cfg: ModelConfig = BASELINE, graph: bool = False, warmup: int = 2,
+                    overlap_wgrad: bool = True, fused_lmhead: bool | None = None, loss_scale: float | None = None):
     """train_step(params, opt_state, batch) -> (params, opt_state, loss).
 
-    Parameters are updated in place; the loss is a 0-d device tensor (no host
-    sync inside the step, as with the jitted step of train.py:328-341).
+    ``optimizer`` is an ``AdamW`` or a ``MultiSteps`` around one (the
+    reference's make_train_step takes the optax optimizer the same way,
+    train.py:328-341). Parameters are updated in place; the loss is a 0-d
+    device tensor (no host sync inside the step, as with the jitted step).
 
-    graph=True: after ``warmup`` eager steps the whole step (forward, backward,
-    AdamW) is captured once into a HIP graph and replayed; the batch is copied
-    into the graph's input buffer and lr / bias corrections are written to the
-    device before each replay.
+    loss_scale (default NLEARN_LOSS_SCALE): the backward starts from
+    d(loss)/d(loss) = loss_scale, so every gradient is scaled by it, and the
+    optimizer divides it out before use (train.py:313-316,332-337); the loss
+    returned is the unscaled one.
+
+    graph=True: after ``warmup`` eager steps the whole step (forward, backward
+    and the optimizer's capturable part) is captured once into a HIP graph
+    and replayed; the batch is copied into the graph's input buffer and the
+    optimizer's scalars are written to the device before each replay.
 
     overlap_wgrad: run the weight-gradient kernels on a second stream beside
     the input-gradient chain (kernels.wgrad); results are identical.
@@ -251,23 +383,27 @@ def make_train_step(optimizer: AdamW, cfg: ModelConfig = BASELINE, graph: bool =
     fused_lmhead: the loss through linear_cross_entropy (see ``batch_loss``).
     """
     overlap = wgrad.overlap_weight_grads if overlap_wgrad else _no_overlap
+    scale = LOSS_SCALE if loss_scale is None else float(loss_scale)
+    if not scale > 0:
+        raise ValueError("make_train_step: loss_scale must be > 0")
 
     def eager_step(params, opt_state, batch):
         for p in tree_leaves(params):
             p.grad = None
         loss = batch_loss(params, batch, cfg, fused_lmhead)
+        seed = None if scale == 1.0 else torch.full((), scale, dtype=torch.float32, device=loss.device)
         # weight gradients run on a second stream beside the dX chain; the
         # contexts join it and finish the LayerNorm parameter sums before the
         # optimizer reads the gradient buffers
         with overlap(loss.device), fused.defer_layer_norm_param_sums():
-            loss.backward()
+            loss.backward(seed)
         with torch.no_grad():
-            opt_state = optimizer.update(params, opt_state)
+            opt_state = optimizer.update(params, opt_state, scale)
         return params, opt_state, loss.detach()
 
     if not graph:
         return eager_step
-    return _GraphedStep(optimizer, cfg, eager_step, warmup, overlap, fused_lmhead)
+    return _GraphedStep(optimizer, cfg, eager_step, warmup, overlap, fused_lmhead, scale)
 
 
 @contextlib.contextmanager
@@ -276,10 +412,11 @@ def _no_overlap(device=None):
 
 
 class _GraphedStep:
-    def __init__(self, optimizer, cfg, eager_step, warmup, overlap, fused_lmhead):
+    def __init__(self, optimizer, cfg, eager_step, warmup, overlap, fused_lmhead, loss_scale):
         self.opt, self.cfg, self.eager_step, self.warmup = optimizer, cfg, eager_step, warmup
         self.overlap = overlap
         self.fused_lmhead = fused_lmhead
+        self.loss_scale = loss_scale
         self.done = 0
         self.graph = None
         self.static_batch = None
@@ -294,9 +431,9 @@ class _GraphedStep:
         for p in leaves:
             p.grad = None
         wgrad.prepare(batch.device)  # create the side stream outside the capture
-        # the backward's seed d(loss)/d(loss) = 1, made once and kept (every
-        # replay reads it): backward() without it records a fill kernel
-        self.seed = seed = torch.ones((), dtype=torch.float32, device=batch.device)
+        # the backward's seed d(loss)/d(loss) (the loss scale), made once and
+        # kept (every replay reads it): backward() without it records a fill kernel
+        self.seed = seed = torch.full((), self.loss_scale, dtype=torch.float32, device=batch.device)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
@@ -304,7 +441,7 @@ class _GraphedStep:
             with self.overlap(loss.device), fused.defer_layer_norm_param_sums():
                 loss.backward(seed)
             with torch.no_grad():
-                self.opt.apply(params, state)
+                self.opt.apply(params, state, self.loss_scale)
         self.static_loss = loss.detach()
         self.graph = g
 
@@ -315,9 +452,11 @@ class _GraphedStep:
                 return self.eager_step(params, state, batch)
             self._capture(params, state, batch)
         self.static_batch.copy_(batch, non_blocking=True)
-        self.opt.prepare(state)
+        self.opt.prepare(state, self.loss_scale)
         self.graph.replay()
-        state["count"] += 1
+        with torch.no_grad():
+            self.opt.finish(params, state)
+        self.opt.advance(state)
         return params, state, self.static_loss.clone()
 
 
@@ -349,9 +488,16 @@ def train(steps: int = 20, seq_len: int = 512, seed: int = 0, batch_size: int = 
     continues from ``resume.pkl`` of ``run_name`` when one exists (parameters,
     optimizer state incl. the schedule position, next step)."""
     cfg = cfg or ModelConfig(max_seq_len=max(seq_len, BASELINE.max_seq_len))
-    warmup = min(WARMUP_STEPS, max(1, steps) // 5)
-    sched = warmup_cosine_decay_schedule(0.0, peak_lr, warmup, max(1, steps), peak_lr / 10)
-    opt = AdamW(sched)
+    # with GRAD_ACCUM micro-steps per update the schedule advances per
+    # effective update (train.py:483-495)
+    eff_updates = max(1, steps // GRAD_ACCUM)
+    warmup = min(WARMUP_STEPS, eff_updates // 5)
+    sched = warmup_cosine_decay_schedule(0.0, peak_lr, warmup, eff_updates, peak_lr / 10)
+    opt = AdamW(sched, clip_norm=GRAD_CLIP)
+    if GRAD_ACCUM > 1:
+        opt = MultiSteps(opt, GRAD_ACCUM)
+        print(f"Gradient accumulation: {GRAD_ACCUM} micro-batches/update "
+              f"(effective batch {batch_size * GRAD_ACCUM}, {eff_updates} updates)")
     start = 0
     resumed = load_resume_state(opt, run_name) if resume else None
     if resumed is not None:

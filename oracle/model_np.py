@@ -238,16 +238,34 @@ def warmup_cosine(count, peak, warmup, decay_steps, end):
     return end + (peak - end) * 0.5 * (1.0 + math.cos(math.pi * frac))
 
 
-class AdamWNP:
-    """optax.adamw: bias-corrected Adam plus decoupled decay lr*wd*p on every leaf."""
+def global_norm(grads) -> float:
+    """optax.global_norm: sqrt of the sum of squares over every leaf."""
+    return float(np.sqrt(sum(float(np.sum(np.square(g, dtype=np.float64))) for g in _leaves(grads))))
 
-    def __init__(self, params, schedule, wd=0.1, b1=0.9, b2=0.999, eps=1e-8):
+
+def clip_by_global_norm(grads, max_norm: float):
+    """optax.clip_by_global_norm(max_norm) (train.py:505-506): the leaves as they
+    are while the global norm is below max_norm, else (g / norm) * max_norm."""
+    n = global_norm(grads)
+    if n < max_norm:
+        return grads
+    return _map(lambda g: (g / g.dtype.type(n)) * g.dtype.type(max_norm), grads)
+
+
+class AdamWNP:
+    """optax.adamw: bias-corrected Adam plus decoupled decay lr*wd*p on every leaf;
+    clip_norm > 0 chains optax.clip_by_global_norm in front (train.py:502-506)."""
+
+    def __init__(self, params, schedule, wd=0.1, b1=0.9, b2=0.999, eps=1e-8, clip_norm=0.0):
         self.schedule, self.wd, self.b1, self.b2, self.eps = schedule, wd, b1, b2, eps
+        self.clip_norm = clip_norm
         self.m = [np.zeros_like(p) for p in _leaves(params)]
         self.v = [np.zeros_like(p) for p in _leaves(params)]
         self.count = 0
 
     def step(self, params, grads):
+        if self.clip_norm > 0:
+            grads = clip_by_global_norm(grads, self.clip_norm)
         lr = self.schedule(self.count)
         t = self.count + 1
         bc1, bc2 = 1 - self.b1 ** t, 1 - self.b2 ** t
@@ -260,14 +278,50 @@ class AdamWNP:
         self.count = t
 
 
-class TrainStepNP:
-    """One full training step (loss + grads + AdamW) on the CPU."""
+class MultiStepsNP:
+    """optax.MultiSteps(inner, every_k_schedule=k) (train.py:319-325,507-508):
+    each call is a micro-step whose gradients join the running mean
+    acc + (g - acc) / (i + 1); every k-th call applies the inner optimizer to
+    that mean and resets it. The inner count (the schedule) advances per update."""
 
-    def __init__(self, params, lr=3e-4, warmup=0, decay_steps=1000, cfg: Config = BASELINE, wd=0.1):
+    def __init__(self, inner: AdamWNP, k: int):
+        self.inner, self.k = inner, k
+        self.acc = None
+        self.mini_step = 0
+
+    def step(self, params, grads):
+        if self.mini_step == 0:
+            self.acc = _map(lambda g: g.copy(), grads)
+        else:
+            n = self.mini_step + 1
+            self.acc = _zip_map(lambda a, g: a + (g - a) / a.dtype.type(n), self.acc, grads)
+        if self.mini_step + 1 == self.k:
+            self.inner.step(params, self.acc)
+            self.mini_step = 0
+        else:
+            self.mini_step += 1
+
+
+def _zip_map(fn, a, b):
+    if isinstance(a, dict):
+        return {k: _zip_map(fn, a[k], b[k]) for k in a}
+    if isinstance(a, list):
+        return [_zip_map(fn, x, y) for x, y in zip(a, b)]
+    return fn(a, b)
+
+
+class TrainStepNP:
+    """One full training step (loss + grads + optimizer) on the CPU; with
+    accum > 1 one call is one micro-step of optax.MultiSteps."""
+
+    def __init__(self, params, lr=3e-4, warmup=0, decay_steps=1000, cfg: Config = BASELINE, wd=0.1, accum=1,
+                 clip_norm=0.0):
         self.params, self.cfg = params, cfg
         sched = (lambda c: lr) if warmup == 0 and decay_steps == 0 else (
             lambda c: warmup_cosine(c, lr, warmup, decay_steps, lr / 10))
-        self.opt = AdamWNP(params, sched, wd=wd)
+        self.opt = AdamWNP(params, sched, wd=wd, clip_norm=clip_norm)
+        if accum > 1:
+            self.opt = MultiStepsNP(self.opt, accum)
 
     def __call__(self, batch):
         loss, grads = loss_and_grads(self.params, batch, self.cfg)

@@ -107,3 +107,49 @@ def test_init_matches_device_initialiser():
     assert len(a) == len(b)
     for x, y in zip(a, b):
         np.testing.assert_array_equal(x, y)
+
+
+def test_clip_by_global_norm_closed_form():
+    """optax.clip_by_global_norm: the norm over all leaves; below the threshold
+    the gradients pass unchanged, above it they are rescaled to norm max_norm
+    with their direction kept."""
+    from oracle import model_np as om
+
+    rng = np.random.default_rng(5)
+    g = {"a": rng.standard_normal((3, 4)).astype(np.float32), "b": [rng.standard_normal(7).astype(np.float32)]}
+    flat = np.concatenate([g["a"].ravel(), g["b"][0]]).astype(np.float64)
+    n = np.linalg.norm(flat)
+    assert abs(om.global_norm(g) - n) < 1e-9 * n
+    same = om.clip_by_global_norm(g, n * 1.01)
+    assert same is g
+    c = om.clip_by_global_norm(g, 0.5)
+    cf = np.concatenate([c["a"].ravel(), c["b"][0]]).astype(np.float64)
+    assert abs(np.linalg.norm(cf) - 0.5) < 1e-6
+    np.testing.assert_allclose(cf * n / 0.5, flat, rtol=1e-6)
+
+
+def test_multisteps_is_adamw_on_the_mean_gradient():
+    """optax.MultiSteps(k=3): parameters unchanged on the first two calls; the
+    third applies AdamW to the mean of the three gradients (the running mean
+    acc + (g - acc)/(i+1) equals it up to rounding); the schedule count moves
+    once per update."""
+    from oracle import model_np as om
+
+    rng = np.random.default_rng(6)
+    p0 = {"w": rng.standard_normal((5, 6)).astype(np.float32), "v": rng.standard_normal(9).astype(np.float32)}
+    gs = [{k: rng.standard_normal(x.shape).astype(np.float32) for k, x in p0.items()} for _ in range(6)]
+    sched = lambda c: 1e-2 * (c + 1)  # noqa: E731
+    pa = {k: x.copy() for k, x in p0.items()}
+    ms = om.MultiStepsNP(om.AdamWNP(pa, sched), 3)
+    pb = {k: x.copy() for k, x in p0.items()}
+    ref = om.AdamWNP(pb, sched)
+    for i, g in enumerate(gs):
+        ms.step(pa, g)
+        if i % 3 != 2:
+            assert all(np.array_equal(pa[k], (p0 if i < 3 else pb)[k]) for k in p0)
+        else:
+            mean = {k: (gs[i - 2][k] + gs[i - 1][k] + gs[i][k]) / np.float32(3) for k in p0}
+            ref.step(pb, mean)
+            for k in p0:
+                np.testing.assert_allclose(pa[k], pb[k], rtol=1e-5, atol=1e-7)
+    assert ms.inner.count == 2 and ref.count == 2
