@@ -80,3 +80,23 @@ def test_library_targets_gfx950_only():
 
     assert "--offload-arch=gfx950" in _build.HIPCC_FLAGS
     assert sum(f.startswith("--offload-arch") for f in _build.HIPCC_FLAGS) == 1
+
+
+def test_jax_ffi_binding_registers_only_defined_handlers():
+    """The reference-side binding (not built here: no JAX / XLA FFI headers):
+    every target register.py registers has a handler symbol defined in
+    nlearn_jax_ffi.cc, every handler is registered, the six reference targets
+    are all there, and every nl_* entry point a handler calls is declared in
+    include/nlearn_hip.h."""
+    from nlearn_amd.jax_ffi import register
+
+    src = (ROOT / "nlearn_amd" / "jax_ffi" / "nlearn_jax_ffi.cc").read_text()
+    code = re.sub(r"//[^\n]*", "", src)
+    defined = set(re.findall(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(\s*(\w+)\s*,", code))
+    registered = {sym for _, sym in register.TARGETS}
+    assert registered == defined
+    targets = {t for t, _ in register.TARGETS}
+    assert {"flash_attention_fwd", "flash_attention_bwd_dq", "flash_attention_bwd_dkdv", "gemm", "ce_fwd",
+            "ce_bwd"} <= targets
+    called = set(re.findall(r"\b(nl_[a-z0-9_]+)\s*\(", code)) - defined
+    assert called and called <= set(header_functions()), called - set(header_functions())
