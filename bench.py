@@ -49,6 +49,16 @@ def _args():
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write profiles/traffic.json from the rocprofv3 CSV output of the two --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) over --traffic-probe")
+    ap.add_argument("--replay-probe", action="store_true",
+                    help="only warm up, capture and replay the graphed step --steps times (for rocprofv3 "
+                         "--kernel-trace: the busy ratio of graph replays)")
+    ap.add_argument("--busy-summary", metavar="TRACE_DIR",
+                    help="write profiles/busy_<workload>.json from the rocprofv3 kernel trace of --replay-probe")
+    ap.add_argument("--flash-probe", nargs=2, type=int, metavar=("N_HEADS", "SEQ"),
+                    help="only run flash forward + backward at (N_HEADS, SEQ, 64) a few times (for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="ARG",
+                    help="OUT.md TITLE DIR [DIR ...]: per-kernel PMC medians from rocprofv3 --pmc CSV dirs, with "
+                         "MFMA busy, VALU/MFMA and LDS bank-conflict ratios")
     return ap.parse_args()
 
 
@@ -154,7 +164,8 @@ def cpu_baseline(seconds: float):
     rng = np.random.default_rng(0)
     batch = rng.integers(0, 50257, (bs, seq + 1)).astype(np.int64)
     t0 = time.time()
-    step(batch)  # warm-up (page-in, BLAS threads)
+    for _ in range(2):  # warm-up (page-in, BLAS threads), as the CPU-baseline plan asks
+        step(batch)
     times = []
     while True:
         t1 = time.time()
@@ -164,8 +175,21 @@ def cpu_baseline(seconds: float):
             break
     t = float(np.median(times))
     return {"value": bs * seq / t, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": _cpu_model(),
             "sample": f"NumPy fp32 restatement of one train step (fwd+bwd+AdamW), bs {bs} x seq {seq}, "
-                      f"median of {len(times)} steps after 1 warm-up; {t:.2f} s/step"}
+                      f"median of {len(times)} steps after 2 warm-ups; {t:.2f} s/step"}
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as 'Model name')."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
@@ -267,6 +291,141 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps({k: v["bytes_per_launch"] for k, v in out["kernels"].items()}))
+
+
+BUSY_FIRST_KERNEL = "embed_fwd_kernel"   # launched once per step, at its start (the embedding lookup)
+
+
+def busy_summary(trace_dir: str, steps: int, bs: int, seq: int) -> None:
+    """Busy ratio of the graphed step from a rocprofv3 kernel trace of
+    --replay-probe: the last ``steps`` step starts (each step's first kernel)
+    delimit the replays; over that window, the union of all kernel intervals
+    (overlapping kernels counted once) over the wall time, plus the plain sum
+    of kernel durations (which exceeds the union where streams overlap) and
+    the per-kernel time per step."""
+    import csv
+    import glob
+
+    rows = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    rows.sort()
+    starts = [t0 for t0, _, name in rows if BUSY_FIRST_KERNEL in name]
+    if len(starts) < steps + 1:
+        raise SystemExit(f"busy-summary: found {len(starts)} step starts, need {steps + 1}")
+    # the window: from the first of the last `steps` step starts to the last kernel's end
+    w0 = starts[-steps]
+    win = [(a, b, n) for a, b, n in rows if a >= w0]
+    w1 = max(b for _, b, _ in win)
+    union, cur0, cur1 = 0, None, None
+    for a, b, _ in win:
+        if cur1 is None or a > cur1:
+            if cur1 is not None:
+                union += cur1 - cur0
+            cur0, cur1 = a, b
+        else:
+            cur1 = max(cur1, b)
+    union += cur1 - cur0
+    total = sum(b - a for a, b, _ in win)
+    per = defaultdict(lambda: [0, 0])
+    for a, b, n in win:
+        short = n.split("(")[0][:90]
+        per[short][0] += b - a
+        per[short][1] += 1
+    wall = w1 - w0
+    out = {"workload": f"train_step fwd+bwd+AdamW d512/8h/4L vocab50257 bs{bs} seq{seq}, hip_graph replays",
+           "command": f"rocprofv3 --kernel-trace --output-format csv -d <dir> -o run -- python3 bench.py "
+                      f"--replay-probe --steps {steps} --batch-size {bs} --seq-len {seq}; "
+                      f"python3 bench.py --busy-summary <dir> --steps {steps} --batch-size {bs} --seq-len {seq}",
+           "replays": steps, "wall_ms_per_step": round(wall / steps / 1e6, 4),
+           "busy_union_ms_per_step": round(union / steps / 1e6, 4),
+           "busy_ratio": round(union / wall, 4),
+           "kernel_sum_ms_per_step": round(total / steps / 1e6, 4),
+           "kernel_sum_over_wall": round(total / wall, 4),
+           "kernels_ms_per_step": {k: {"ms": round(v[0] / steps / 1e6, 4), "calls": round(v[1] / steps, 2)}
+                                   for k, v in sorted(per.items(), key=lambda kv: -kv[1][0])}}
+    path = os.path.join(os.path.dirname(TRAFFIC_FILE), f"busy_bs{bs}_seq{seq}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps({k: out[k] for k in ("wall_ms_per_step", "busy_union_ms_per_step", "busy_ratio",
+                                          "kernel_sum_over_wall")}))
+
+
+def flash_probe(n: int, S: int, reps: int = 5) -> None:
+    """BASELINE configs[1] flash forward and backward at (n, S, 64), bf16
+    N(0,1) inputs, ``reps`` times each: the preprocess, dK/dV and dQ kernels
+    run as in nl_flash_attention_bwd (one stream)."""
+    import torch
+
+    from nlearn_amd import _lib
+    from nlearn_amd.attention import flash_bwd_raw4, flash_fwd_raw4
+
+    _lib.load()
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    q, k, v, do = (torch.randn((n // 8, 8, S, 64), generator=g, device=dev).to(torch.bfloat16) for _ in range(4))
+    for _ in range(reps):
+        O, L = flash_fwd_raw4(q, k, v)
+        flash_bwd_raw4(q, k, v, O, do, L)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "flash", "shape": [n, S, 64], "reps": reps}))
+
+
+def pmc_summary(out_md: str, title: str, dirs) -> None:
+    """Median of every counter per kernel over the dispatches in the rocprofv3
+    --pmc CSV output of ``dirs`` (one directory per counter pass), as a
+    markdown table, with the derived ratios used in the design notes:
+    MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 x CUs x 4 SIMDs)
+    (rocprofv3 sums GRBM_GUI_ACTIVE over the 8 XCDs, and the MFMA busy cycles
+    over every SIMD; this reproduces flops / (time x peak) at the measured clock),
+    VALU instructions per MFMA, LDS bank conflicts per LDS active cycle."""
+    import csv
+    import glob
+    import statistics
+
+    per = defaultdict(lambda: defaultdict(list))
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if "nl::" not in r["Kernel_Name"]:
+                    continue
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("nl::", "")
+                name = name.replace("void ", "").split("(")[0]
+                per[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    cus = 256
+    lines = [f"# {title}", "", "Medians over the dispatches of each kernel (rocprofv3 --pmc, one pass per "
+             "counter set). MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 256 CUs x 4 "
+             "SIMDs); LDS conflict = SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE; cycles = GRBM_GUI_ACTIVE / 8.",
+             ""]
+    counters = sorted({c for k in per.values() for c in k})
+    lines.append("| kernel | cycles | MFMA busy | VALU / MFMA | LDS / MFMA | LDS conflict | "
+                 + " | ".join(counters) + " |")
+    lines.append("|---|---:|---:|---:|---:|---:|" + "---:|" * len(counters))
+    for name, cs in sorted(per.items()):
+        med = {c: statistics.median(v) for c, v in cs.items()}
+        busy = med.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) / (med["GRBM_GUI_ACTIVE"] / 8 * cus * 4) \
+            if med.get("GRBM_GUI_ACTIVE") else float("nan")
+        vpm = med["SQ_INSTS_VALU"] / med["SQ_INSTS_MFMA"] if med.get("SQ_INSTS_MFMA") else float("nan")
+        conf = med["SQ_LDS_BANK_CONFLICT"] / med["SQ_LDS_IDX_ACTIVE"] if med.get("SQ_LDS_IDX_ACTIVE") else float("nan")
+        lpm = med["SQ_INSTS_LDS"] / med["SQ_INSTS_MFMA"] if med.get("SQ_INSTS_MFMA") else float("nan")
+        cyc = med.get("GRBM_GUI_ACTIVE", float("nan")) / 8
+        lines.append(f"| `{name[:60]}` | {cyc:.0f} | {busy:.3f} | {vpm:.2f} | {lpm:.2f} | {conf:.3f} | "
+                     + " | ".join(f"{med[c]:.4g}" if c in med else "" for c in counters) + " |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def load_busy(bs: int, seq: int):
+    """The committed busy-ratio summary of this workload, if any."""
+    try:
+        with open(os.path.join(os.path.dirname(TRAFFIC_FILE), f"busy_bs{bs}_seq{seq}.json")) as f:
+            b = json.load(f)
+        return {"busy_ratio": b["busy_ratio"], "wall_ms_per_step": b["wall_ms_per_step"],
+                "source": f"profiles/busy_bs{bs}_seq{seq}.json (rocprofv3 kernel trace of graph replays)"}
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def load_traffic(tag: str):
@@ -479,6 +638,15 @@ def main():
     if a.traffic_summary:
         traffic_summary(*a.traffic_summary)
         return
+    if a.busy_summary:
+        busy_summary(a.busy_summary, a.steps, a.batch_size, a.seq_len)
+        return
+    if a.flash_probe:
+        flash_probe(*a.flash_probe)
+        return
+    if a.pmc_summary:
+        pmc_summary(a.pmc_summary[0], a.pmc_summary[1], a.pmc_summary[2:])
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the data-parallel step would all-reduce "
               "the gradients over RCCL before AdamW). Run with --gpus 1.", file=sys.stderr)
@@ -513,6 +681,12 @@ def main():
         params, state, loss = step(params, state, batches[i % 4])
     torch.cuda.synchronize()
     torch.cuda.reset_peak_memory_stats()
+    if a.replay_probe:
+        for i in range(a.steps):
+            params, state, loss = step(params, state, batches[i % 4])
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": "replay", "steps": a.steps, "loss": round(float(loss), 4)}))
+        return
 
     probe.enabled = not graph
     torch.cuda.synchronize()
@@ -525,28 +699,48 @@ def main():
         # Per-kernel durations: events cannot be placed between the nodes of a
         # replayed graph (torch-ROCm refuses external events in a capture), so
         # the same step runs a.steps more times eagerly, every kernel bracketed
-        # by events on its launch stream; kernels and shapes are identical.
+        # by events on its launch stream; kernels, shapes and the two-stream
+        # overlap are those of the replays.
         eager = make_train_step(opt, cfg, graph=False, fused_lmhead=a.fused_lmhead)
         probe.enabled = True
         for i in range(a.steps):
             params, state, loss = eager(params, state, batches[i % 4])
         torch.cuda.synchronize()
     probe.enabled = False
+    # The same step once more on one stream (no weight-gradient overlap): every
+    # kernel alone on the GPU, its own speed without CUs shared with the other
+    # stream.
+    iso_probe = KernelProbe(torch)
+    _lib.set_probe(iso_probe)
+    solo = make_train_step(opt, cfg, graph=False, fused_lmhead=a.fused_lmhead, overlap_wgrad=False)
+    iso_steps = min(a.steps, 5)
+    iso_probe.enabled = True
+    for i in range(iso_steps):
+        params, state, loss = solo(params, state, batches[i % 4])
+    torch.cuda.synchronize()
+    iso_probe.enabled = False
     _lib.set_probe(None)
 
     tokens = bs * seq
     ms = dt / a.steps * 1e3
     value = tokens * a.steps / dt
     kernels = probe.summary(a.steps)
+    iso = iso_probe.summary(iso_steps)
     dom_tag = max(kernels, key=lambda k: kernels[k]["time_per_step_ms"]) if kernels else None
     roof = None
     if dom_tag:
         k = kernels[dom_tag]
         roof = {"bound": k["bound"], "achieved": round(k["achieved"], 2), "peak": k["peak"], "unit": k["unit"],
                 "frac": round(k["frac"], 4), "traffic": load_traffic(dom_tag), "kernel": dom_tag,
-                "avg_us": round(k["avg_us"], 2)}
+                "avg_us": round(k["avg_us"], 2),
+                "timing": "in the step: HIP events on the launch stream, two-stream overlap as in the replays",
+                "frac_isolated": round(iso[dom_tag]["frac"], 4) if dom_tag in iso else None,
+                "avg_us_isolated": round(iso[dom_tag]["avg_us"], 2) if dom_tag in iso else None}
     fl = flops_per_step(cfg, bs, seq)
-    probed_ms = sum(k["time_per_step_ms"] for k in kernels.values())
+
+    def _table(kk):
+        return {k: {kk2: (round(vv, 4) if isinstance(vv, float) else vv) for kk2, vv in v.items()}
+                for k, v in sorted(kk.items(), key=lambda kv: -kv[1]["time_per_step_ms"])}
     out = {
         "metric": "train tokens/sec d512/4L/seq512 bs32 (1 GPU)",
         "value": round(value, 1),
@@ -571,10 +765,10 @@ def main():
             "matmul_tflop_per_step": round(fl["total"] / 1e12, 4),
             "six_n_t_tflops": round(fl["six_n_t"] / (dt / a.steps) / 1e12, 2),
             "peak_hbm_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
-            "nlearn_kernels_busy_ratio": round(probed_ms / ms, 4),
+            "busy": load_busy(bs, seq),
             "final_loss": round(float(loss.detach()), 4),
-            "kernels": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                        for k, v in sorted(kernels.items(), key=lambda kv: -kv[1]["time_per_step_ms"])},
+            "kernels_in_step": _table(kernels),
+            "kernels_isolated": _table(iso),
         },
     }
     if not a.no_cpu_baseline:
