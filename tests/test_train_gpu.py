@@ -143,3 +143,30 @@ def test_resume_state_continues_the_step(dev, tmp_path, monkeypatch):
     rest = train(steps=6, seq_len=64, batch_size=2, log_every=100, cfg=small, run_name="t", resume=True,
                  checkpoint_every=2)
     assert len(rest) == 3 and np.isfinite(rest).all()
+
+
+def test_full_gradient_finite_at_seq_8192_both_loss_paths(dev):
+    """The reference's check_grad_nan.py: the whole gradient at seq 8192, bs 1
+    (flash at (8, 8192, 64) per layer), through the LM head + CE and through
+    linear_cross_entropy. Every parameter gradient is finite, the two losses
+    agree within 1e-3 and the gradients within rel-L2 1e-2 (the two paths
+    round the logits identically; they differ only in summation order)."""
+    import torch
+    from nlearn_amd.model import ModelConfig, init_model, tree_leaves
+    from nlearn_amd.train import batch_loss
+
+    cfg = ModelConfig(max_seq_len=8192)
+    batch = torch.from_numpy(np.random.default_rng(0).integers(0, 50257, (1, 8193)).astype(np.int32)).to(dev)
+    out = []
+    for fused in (False, True):
+        params = init_model(0, cfg, dev)
+        loss = batch_loss(params, batch, cfg, fused_lmhead=fused)
+        loss.backward()
+        torch.cuda.synchronize()
+        grads = [p.grad.float().cpu().numpy() for p in tree_leaves(params)]
+        for i, g in enumerate(grads):
+            assert np.isfinite(g).all(), (fused, i)
+        out.append((loss.item(), grads))
+    assert abs(out[0][0] - out[1][0]) < 1e-3
+    for i, (a, b) in enumerate(zip(out[0][1], out[1][1])):
+        assert rel_l2(b, a, floor=1e-8) < 1e-2, i
