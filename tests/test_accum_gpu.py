@@ -187,3 +187,42 @@ def test_model_accum_clip_loss_scale_curve_matches_oracle(dev):
     cpu = [ref(b.astype(np.int64)) for b in batches]
     print("gpu", np.round(gpu, 5).tolist(), "cpu", np.round(cpu, 5).tolist())
     assert np.abs(np.array(gpu) - np.array(cpu)).max() < 1e-2
+
+
+def test_multisteps_resume_mid_accumulation(dev, tmp_path, monkeypatch):
+    """save_resume_state after 3 micro-steps of MultiSteps(k = 2) (one update
+    done, one micro-step accumulated), then load_resume_state into a fresh
+    optimizer: the next micro-steps give the uninterrupted run's losses and
+    parameters (the mini-step and the running mean travel in resume.pkl)."""
+    import torch
+    from nlearn_amd.model import ModelConfig, init_model, tree_leaves
+    from nlearn_amd.train import AdamW, MultiSteps, load_resume_state, make_train_step, save_resume_state
+
+    monkeypatch.chdir(tmp_path)
+    cfg = ModelConfig(max_seq_len=64)
+    rng = np.random.default_rng(97)
+    batches = [torch.from_numpy(rng.integers(0, 50257, (2, 65)).astype(np.int32)).to(dev) for _ in range(6)]
+    sched = lambda c: 1e-3  # noqa: E731
+    opt = MultiSteps(AdamW(sched), 2)
+    params = init_model(0, cfg, dev)
+    state = opt.init(params)
+    step = make_train_step(opt, cfg)
+    for b in batches[:3]:
+        params, state, _ = step(params, state, b)
+    assert state["mini_step"] == 1 and state["count"] == 1
+    save_resume_state(params, state, 3, run_name="ms")
+    la = []
+    for b in batches[3:]:
+        params, state, loss = step(params, state, b)
+        la.append(float(loss))
+    opt2 = MultiSteps(AdamW(sched), 2)
+    params2, state2, nxt = load_resume_state(opt2, run_name="ms", device=dev)
+    assert nxt == 3 and state2["mini_step"] == 1 and state2["count"] == 1 and state2["inner"]["count"] == 1
+    step2 = make_train_step(opt2, cfg)
+    lb = []
+    for b in batches[3:]:
+        params2, state2, loss = step2(params2, state2, b)
+        lb.append(float(loss))
+    np.testing.assert_allclose(lb, la, rtol=1e-6, atol=1e-6)
+    for a, c in zip(tree_leaves(params), tree_leaves(params2)):
+        assert rel_l2(c.detach().cpu().numpy(), a.detach().cpu().numpy()) < 1e-5
