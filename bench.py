@@ -29,8 +29,8 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 def _args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--batch-size", type=int, default=32)
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -296,6 +296,13 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
 BUSY_FIRST_KERNEL = "embed_fwd_kernel"   # launched once per step, at its start (the embedding lookup)
 
 
+def _kernel_short_name(name: str) -> str:
+    """A demangled kernel name without namespaces, ``void`` and the argument
+    list (template arguments kept, so tile configurations stay distinct)."""
+    name = name.replace("(anonymous namespace)::", "").replace("nl::", "").replace("void ", "")
+    return name.split("(")[0][:110]
+
+
 def busy_summary(trace_dir: str, steps: int, bs: int, seq: int) -> None:
     """Busy ratio of the graphed step from a rocprofv3 kernel trace of
     --replay-probe: the last ``steps`` step starts (each step's first kernel)
@@ -330,7 +337,7 @@ def busy_summary(trace_dir: str, steps: int, bs: int, seq: int) -> None:
     total = sum(b - a for a, b, _ in win)
     per = defaultdict(lambda: [0, 0])
     for a, b, n in win:
-        short = n.split("(")[0][:90]
+        short = _kernel_short_name(n)
         per[short][0] += b - a
         per[short][1] += 1
     wall = w1 - w0
@@ -390,8 +397,7 @@ def pmc_summary(out_md: str, title: str, dirs) -> None:
             for r in csv.DictReader(open(f)):
                 if "nl::" not in r["Kernel_Name"]:
                     continue
-                name = r["Kernel_Name"].replace("(anonymous namespace)::", "").replace("nl::", "")
-                name = name.replace("void ", "").split("(")[0]
+                name = _kernel_short_name(r["Kernel_Name"])
                 per[name][r["Counter_Name"]].append(float(r["Counter_Value"]))
     cus = 256
     lines = [f"# {title}", "", "Medians over the dispatches of each kernel (rocprofv3 --pmc, one pass per "
