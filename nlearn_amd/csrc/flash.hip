@@ -221,18 +221,29 @@ struct FwdArgs {
   float* L;
 };
 
-// Store a 32x32 transposed accumulator pair (d tiles 0/1) for the lane's row:
-// lane (row, g) holds columns dt*32 + 8qq + 4g + t.
-__device__ __forceinline__ void store_row64(uint16_t* rowp, const f32x16 acc[2], float mul, int g) {
+// Store a wave's 32 rows x 64 columns (a transposed accumulator pair: lane
+// (row l32, g) holds columns dt*32 + 8qq + 4g + t in acc[dt][4qq + t]) through
+// a 4 KB LDS slab, so that each store instruction writes
+// whole 128-byte rows (16 bytes per lane) instead of 8 bytes in each of 32 rows.
+// Slab row r holds its 16-byte chunk c at slot c ^ (r & 7). Rows at or past S
+// are not stored. The caller makes sure no other wave still reads the slab.
+__device__ __forceinline__ void store_rows_staged(uint16_t* slab, const f32x16 acc[2], float mul, int g, int l32,
+                                                  int lane, const OutOp& out, int b, int h, int row0, int S) {
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
-      const int col = dt * 32 + qq * 8 + 4 * g;
-      *reinterpret_cast<u32x2*>(rowp + col) =
+      const int c = dt * 4 + qq;  // columns 8c + 4g .. 8c + 4g + 3
+      *reinterpret_cast<u32x2*>(slab + l32 * 64 + ((c ^ (l32 & 7)) << 3) + 4 * g) =
           u32x2{pack_bf16x2(acc[dt][4 * qq] * mul, acc[dt][4 * qq + 1] * mul),
                 pack_bf16x2(acc[dt][4 * qq + 2] * mul, acc[dt][4 * qq + 3] * mul)};
     }
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int r = it * 8 + (lane >> 3), c = lane & 7;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(slab + r * 64 + ((c ^ (r & 7)) << 3));
+    if (row0 + r < S) *reinterpret_cast<u32x4*>(out.at(b, h, row0 + r) + c * 8) = v;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -359,31 +370,29 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
   }
 
   const float lt = l + __shfl_xor(l, 32, kWave);
-  if (qvalid) {
-    const float inv = 1.f / lt;
-    store_row64(a.o.at(b, h, q), o, inv, g);
-    if (g == 0) a.L[((int64_t)b * a.H + h) * S + q] = (m + fast_log2(lt)) * kLn2;
-  }
+  const float inv = qvalid ? 1.f / lt : 0.f;
+  if (qvalid && g == 0) a.L[((int64_t)b * a.H + h) * S + q] = (m + fast_log2(lt)) * kLn2;
+  __syncthreads();  // every wave is done reading the K / V blocks
+  store_rows_staged(wave == 0 ? sK0 : wave == 1 ? sK1 : wave == 2 ? sV0 : sV1, o, inv, g, l32, lane, a.o, b, h, qw0,
+                    S);
 }
 
 // ---------------------------------------------------------------------------
 // backward preprocess: D = rowsum(dO o O)
 // ---------------------------------------------------------------------------
 struct PreArgs {
-  int S, H, rows;
+  int S, H;
   Op o, dout;
   float* D;
 };
+// grid (ceil(S / 32), H, B): 32 rows per workgroup, 8 lanes per row, 16 bytes
+// of O and of dO per lane; no division in the index math
 __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(PreArgs a) {
-  // 8 lanes per row, 16 bytes each
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t row = gid >> 3;
-  const int part = (int)(gid & 7);
+  const int s = (int)blockIdx.x * 32 + ((int)threadIdx.x >> 3);
+  const int part = (int)threadIdx.x & 7;
+  const int h = (int)blockIdx.y, b = (int)blockIdx.z;
   float acc = 0.f;
-  if (row < a.rows) {
-    const int s = (int)(row % a.S);
-    const int bh = (int)(row / a.S);
-    const int h = bh % a.H, b = bh / a.H;
+  if (s < a.S) {
     const u32x4 x = *reinterpret_cast<const u32x4*>(a.o.at(b, h, s) + part * 8);
     const u32x4 y = *reinterpret_cast<const u32x4*>(a.dout.at(b, h, s) + part * 8);
 #pragma unroll
@@ -392,7 +401,7 @@ __global__ __launch_bounds__(256) void flash_bwd_pre_kernel(PreArgs a) {
   acc += __shfl_xor(acc, 1, kWave);
   acc += __shfl_xor(acc, 2, kWave);
   acc += __shfl_xor(acc, 4, kWave);
-  if (row < a.rows && part == 0) a.D[row] = acc;
+  if (s < a.S && part == 0) a.D[((int64_t)b * a.H + h) * a.S + s] = acc;
 }
 
 struct BwdArgs {
@@ -546,10 +555,10 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(BwdArgs a) 
     if (qb + 2 < nqb) issue(sQ0, sO0, sL0, sD0, qb + 2);
     compute(sQ1, sO1, sL1, sD1, qb + 1);
   }
-  if (kvalid) {
-    store_row64(a.dk.at(b, h, key), dk, a.scale, g);
-    store_row64(a.dv.at(b, h, key), dv, 1.f, g);
-  }
+  __syncthreads();  // every wave is done reading the Q / dO blocks
+  uint16_t* slab = wave == 0 ? sQ0 : wave == 1 ? sQ1 : wave == 2 ? sO0 : sO1;
+  store_rows_staged(slab, dk, a.scale, g, l32, lane, a.dk, b, h, kw0, S);
+  store_rows_staged(slab + 32 * kD, dv, 1.f, g, l32, lane, a.dv, b, h, kw0, S);
 }
 
 // ---------------------------------------------------------------------------
@@ -649,7 +658,20 @@ __global__ __launch_bounds__(kThreads, 3) void flash_bwd_dq_kernel(BwdArgs a) {
     if (kb + 2 < nkb) issue(sK0, sV0, kb + 2);
     compute(sK1, sV1, kb + 1);
   }
-  if (qvalid) store_row64(a.dq.at(b, h, q), dq, a.scale, g);
+  // Direct 8-byte stores (lane = row): measured faster here than staging
+  // through LDS, which needs a barrier that makes the waves with less causal
+  // work wait for the others.
+  if (qvalid) {
+#pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int col = dt * 32 + qq * 8 + 4 * g;
+        *reinterpret_cast<u32x2*>(a.dq.at(b, h, q) + col) =
+            u32x2{pack_bf16x2(dq[dt][4 * qq] * a.scale, dq[dt][4 * qq + 1] * a.scale),
+                  pack_bf16x2(dq[dt][4 * qq + 2] * a.scale, dq[dt][4 * qq + 3] * a.scale)};
+      }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -726,13 +748,11 @@ extern "C" int nl_flash_attention_bwd_preprocess(void* stream, int batch, int he
   PreArgs a;
   a.S = seq;
   a.H = heads;
-  a.rows = batch * heads * seq;
   a.o = Op{O, so};
   a.dout = Op{dO, sdo};
   a.D = D;
-  const int64_t threads = (int64_t)a.rows * 8;
-  hipLaunchKernelGGL(flash_bwd_pre_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, a);
+  hipLaunchKernelGGL(flash_bwd_pre_kernel, dim3((unsigned)((seq + 31) / 32), (unsigned)heads, (unsigned)batch),
+                     dim3(256), 0, (hipStream_t)stream, a);
   return nl_check_launch("nl_flash_attention_bwd_preprocess");
 }
 

@@ -144,8 +144,14 @@ def test_colsum_exact_integers(dev, rows, cols):
 # ---------------------------------------------------------------------------
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 8, 16), (100, 1001, 70), (512, 2048, 512), (256, 512, 4096)])
-def test_gemm_bias_and_gelu_epilogues(dev, M, N, K):
+@pytest.mark.parametrize("opB", ["N", "T"])
+@pytest.mark.parametrize("M,N,K", [(1, 8, 16), (100, 1001, 70), (300, 520, 256), (512, 2048, 512),
+                                   (256, 512, 4096)])
+def test_gemm_bias_and_gelu_epilogues(dev, M, N, K, opB):
+    """Bias, bias+GELU and GELU' epilogues, exact on integer inputs. With B
+    stored [N, K] (opB "T", 64-k stages) and K a multiple of 64, the GELU'
+    epilogue's saved tile is fetched during the last K stage; K = 16 and 70
+    take the post-loop fetch; K = 4096 splits K (epilogue after the reduction)."""
     import torch
     from nlearn_amd.kernels.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU, gemm_raw, padded_empty
 
@@ -153,15 +159,18 @@ def test_gemm_bias_and_gelu_epilogues(dev, M, N, K):
     A = rng.integers(-2, 3, (M, K)).astype(np.float32)
     B = rng.integers(-2, 3, (K, N)).astype(np.float32)
     bias = rng.integers(-20, 21, N).astype(np.float32) / 4      # exact quarters
-    Ad, Bd, biasd = _dev_bf16(A, dev), _dev_bf16(B, dev), _f32(bias, dev)
+    Ad, biasd = _dev_bf16(A, dev), _f32(bias, dev)
+    Bd = _dev_bf16(B if opB == "N" else np.ascontiguousarray(B.T), dev)
     acc = ops.gemm(A, B) + bias                                   # exact (integers / quarters < 2^24)
 
-    c = gemm_raw(Ad, Bd, epi=EPI_BIAS, bias=biasd)                 # fp32 out
-    cb = gemm_raw(Ad, Bd, out_dtype=torch.bfloat16, epi=EPI_BIAS, bias=biasd)
+    c = gemm_raw(Ad, Bd, "N", opB, epi=EPI_BIAS, bias=biasd)                 # fp32 out
+    cb = gemm_raw(Ad, Bd, "N", opB, out_dtype=torch.bfloat16, epi=EPI_BIAS, bias=biasd)
     u = padded_empty(M, N, torch.bfloat16, dev)
-    h = gemm_raw(Ad, Bd, out=padded_empty(M, N, torch.bfloat16, dev), epi=EPI_BIAS_GELU, bias=biasd, aux=u)
+    h = gemm_raw(Ad, Bd, "N", opB, out=padded_empty(M, N, torch.bfloat16, dev), epi=EPI_BIAS_GELU, bias=biasd,
+                 aux=u)
     # backward form: C = (A . B) * gelu'(u) with a scaled product so gelu' varies
-    hs = gemm_raw(Ad, Bd, out_dtype=torch.float32, alpha=0.25, epi=EPI_DGELU, aux=u)
+    hs = gemm_raw(Ad, Bd, "N", opB, out_dtype=torch.float32, alpha=0.25, epi=EPI_DGELU, aux=u)
+    hb = gemm_raw(Ad, Bd, "N", opB, out_dtype=torch.bfloat16, alpha=0.25, epi=EPI_DGELU, aux=u)
     torch.cuda.synchronize()
     assert np.array_equal(_np(c), acc)
     assert np.array_equal(_np(cb), ops.bf16_round(acc))
@@ -172,6 +181,8 @@ def test_gemm_bias_and_gelu_epilogues(dev, M, N, K):
     assert np.abs(_np(h) - g_ref).max() <= np.abs(g_ref).max() * 2 ** -8 + 1e-6
     d_ref = om._gelu_bwd(0.25 * ops.gemm(A, B), u_ref.astype(np.float64), t)
     assert rel_l2(_np(hs), d_ref) <= 1e-5
+    # the bf16 output is the fp32 one rounded once
+    assert np.array_equal(_np(hb), ops.bf16_round(_np(hs)))
 
 
 def test_gemm_epilogues_with_split_k(dev):
