@@ -120,9 +120,9 @@ def test_graphed_step_matches_eager(dev):
 @pytest.mark.parametrize("graph", [False, True], ids=["eager", "hip_graph"])
 def test_overlapped_weight_grads_are_bit_identical(dev, graph):
     """Weight gradients forked onto a second stream (kernels.wgrad) change the
-    schedule only: losses and parameters after 4 steps equal the one-stream
-    step bit for bit (a missed join or a buffer recycled under the side stream
-    would show up as a difference)."""
+    schedule only: losses, parameters, moments and bf16 shadows after 4 steps
+    equal the one-stream step bit for bit (a missed join or a buffer recycled
+    under the side stream would show up as a difference)."""
     import torch
     from nlearn_amd.model import ModelConfig, init_model, tree_leaves
     from nlearn_amd.train import AdamW, make_train_step, warmup_cosine_decay_schedule
@@ -142,7 +142,11 @@ def test_overlapped_weight_grads_are_bit_identical(dev, graph):
             params, state, loss = step(params, state, b)
             losses.append(float(loss))
         torch.cuda.synchronize()
-        runs[overlap] = (losses, [p.detach().clone() for p in tree_leaves(params)])
+        leaves = tree_leaves(params)
+        shadows = [sh.clone() for sh in (getattr(p, "_nl_bf16", None) for p in leaves) if sh is not None]
+        runs[overlap] = (losses, [p.detach().clone() for p in leaves] + [t.clone() for t in state["mu"] + state["nu"]]
+                         + shadows)
     assert runs[True][0] == runs[False][0]
+    assert len(runs[True][1]) == len(runs[False][1])
     for a, b in zip(runs[False][1], runs[True][1]):
         assert torch.equal(a, b)
