@@ -28,7 +28,9 @@ import os
 import torch
 
 from .. import _lib
-from .gemm import _check_device, _kernel_ready, bf16_shadow, gemm_raw, grad_buffer, padded_empty, weight_grad
+from . import wgrad
+from .gemm import (_check_device, _kernel_ready, bf16_shadow, gemm_raw, grad_buffer, linear_backward, padded_empty,
+                   weight_grad)
 
 _BF16 = torch.bfloat16
 
@@ -142,6 +144,73 @@ def cross_entropy(logits: torch.Tensor, targets: torch.Tensor, inplace: bool = F
     x = _as_rows(logits)
     out = _CE.apply(x, targets, inplace)
     return out
+
+
+# ---------------------------------------------------------------------------
+# LM head + cross-entropy with the CE pipelined behind the logits GEMM
+# ---------------------------------------------------------------------------
+
+
+class _LMHeadCE(torch.autograd.Function):
+    """logits = X . W in row chunks; each chunk's single CE pass (loss, lse and
+    dlogits written over the logits) runs on a second stream while the GEMM
+    computes the next chunk, so the HBM-bound CE hides behind the MFMA-bound
+    GEMM. Rows are independent in both kernels, and the CE scale is 1/M of
+    all rows, so every value equals the unchunked linear + cross_entropy bit
+    for bit. The backward is linear's, from dlogits scaled by the cotangent."""
+
+    @staticmethod
+    def forward(ctx, x2, W, targets, chunks):
+        Wb = bf16_shadow(W)
+        M, V = x2.shape[0], Wb.shape[1]
+        t = _targets(targets)
+        if t.numel() != M:
+            raise ValueError(f"lm_head_cross_entropy: {t.numel()} targets for {M} rows")
+        _check_device(x2, t)
+        logits = padded_empty(M, V, _BF16, x2.device)
+        ld = _ld(logits)
+        loss_rows = torch.empty(M, dtype=torch.float32, device=x2.device)
+        lse = torch.empty(M, dtype=torch.float32, device=x2.device)
+        main = torch.cuda.current_stream(x2.device)
+        aux = wgrad._side_stream(x2.device, 1)
+        n = max(1, min(int(chunks), M))
+        bounds = [M * i // n for i in range(n + 1)]
+        for r0, r1 in zip(bounds[:-1], bounds[1:]):
+            if r1 == r0:
+                continue
+            gemm_raw(x2[r0:r1], Wb, out=logits[r0:r1])
+            # everything these CE launches touch was allocated above, on the
+            # current stream, and stays referenced until the join below
+            aux.wait_stream(main)
+            with torch.cuda.stream(aux):
+                _lib.call("nl_ce_fwd_bwd", aux.cuda_stream, r1 - r0, V, logits[r0].data_ptr(), ld, t[r0].data_ptr(),
+                          loss_rows[r0].data_ptr(), lse[r0].data_ptr(), 1.0 / M, logits[r0].data_ptr(), ld)
+        main.wait_stream(aux)
+        ctx.save_for_backward(x2, W)
+        ctx.wb = Wb
+        ctx.d = logits
+        ctx.mark_non_differentiable(lse)
+        return mean(loss_rows)
+
+    @staticmethod
+    def backward(ctx, g):
+        x2, W = ctx.saved_tensors
+        d = ctx.d
+        ctx.d = None
+        scale_by_device_scalar_(d, g)
+        dx, dW = linear_backward(x2, W, ctx.wb, d, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
+        return dx, dW, None, None
+
+
+def lm_head_cross_entropy(X: torch.Tensor, W: torch.Tensor, targets: torch.Tensor, chunks: int = 4) -> torch.Tensor:
+    """Mean CE of logits = X . W (X [..., d] bf16, W [d, V]) against ``targets``,
+    equal to ``cross_entropy(linear(X, W), targets, inplace=True)`` bit for
+    bit; with ``chunks`` > 1 row chunks, the CE of one chunk overlaps the GEMM
+    of the next (see _LMHeadCE)."""
+    if X.dim() < 2 or W.dim() != 2:
+        raise ValueError("lm_head_cross_entropy: X needs >= 2 dims and W exactly 2")
+    x2 = X.reshape(-1, X.shape[-1])
+    return _LMHeadCE.apply(x2, W, targets.reshape(-1), int(chunks))
 
 
 # ---------------------------------------------------------------------------

@@ -234,6 +234,22 @@ def matmul(A: torch.Tensor, B: torch.Tensor) -> torch.Tensor:
 # ---------------------------------------------------------------------------
 
 
+def linear_backward(x2, W, Wb, dy, need_dx: bool = True, need_dW: bool = True):
+    """(dX, dW) of Y = X . W from dY: dX = dY . W^T on the current stream, dW =
+    X^T . dY into W's gradient buffer (forked onto the weight-gradient stream
+    when one is active; dW is then None) or returned."""
+    dx = dW = None
+    if need_dx:
+        dx = gemm_raw(dy, Wb, "N", "T", out_dtype=x2.dtype)             # dY . W^T
+    if need_dW:
+        mg = grad_buffer(W)
+        if mg is not None:
+            weight_grad(x2, dy, mg)                                            # X^T . dY -> main_grad
+        else:
+            dW = gemm_raw(x2, dy, "T", "N", out_dtype=_F32 if W.dtype == _F32 else W.dtype)
+    return dx, dW
+
+
 class _Linear(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x2, W):
@@ -247,17 +263,7 @@ class _Linear(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy):
         x2, W = ctx.saved_tensors
-        Wb = ctx.wb
-        dx = dW = None
-        if ctx.needs_input_grad[0]:
-            dx = gemm_raw(dy, Wb, "N", "T", out_dtype=x2.dtype)             # dY . W^T
-        if ctx.needs_input_grad[1]:
-            mg = grad_buffer(W)
-            if mg is not None:
-                weight_grad(x2, dy, mg)                                            # X^T . dY -> main_grad
-            else:
-                dW = gemm_raw(x2, dy, "T", "N", out_dtype=_F32 if W.dtype == _F32 else W.dtype)
-        return dx, dW
+        return linear_backward(x2, W, ctx.wb, dy, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
 
 
 def linear(x: torch.Tensor, W: torch.Tensor) -> torch.Tensor:
