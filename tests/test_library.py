@@ -73,6 +73,27 @@ def test_status_strings_and_argument_errors_without_gpu():
     assert lib.nl_colsum_ws_bytes(16384, 2048) == 256 * 2048 * 4
     assert lib.nl_colsum_bf16(None, 8, 8, 256, 12, 512, 0, 768, 4096) == _lib.NL_EALIGN
     assert lib.nl_embedding_fwd(None, 2, 8, 6, 100, 256, 512, 768, 1024) == _lib.NL_EINVAL
+    # optimizer-side entry points: accumulation, global norm, clipped update
+    assert lib.nl_grad_accumulate(None, 0, None, None, None) == _lib.NL_OK            # nothing to do
+    assert lib.nl_grad_accumulate(None, -1, None, None, None) == _lib.NL_EINVAL
+    assert lib.nl_grad_accumulate(None, 8, 256, None, 512) == _lib.NL_EINVAL
+    assert lib.nl_grad_accumulate(None, 8, 260, 512, 768) == _lib.NL_EALIGN
+    assert lib.nl_global_norm_ws_bytes(1 << 20) >= 1024 * 4
+    assert lib.nl_global_norm(None, -1, None, 256, None, 0) == _lib.NL_EINVAL
+    assert lib.nl_global_norm(None, 8, 256, None, 512, 1 << 16) == _lib.NL_EINVAL          # no output
+    assert lib.nl_global_norm(None, 1 << 20, 256, 512, 768, 16) == _lib.NL_EINVAL          # workspace
+    assert b"workspace" in lib.nl_last_error()
+    assert lib.nl_global_norm(None, 8, 260, 512, 768, 1 << 16) == _lib.NL_EALIGN
+    assert lib.nl_adamw_multi_clip(None, 1, 256, 1, 512, 0.9, 0.999, 1e-8, 0.1, 768, 0.0) == _lib.NL_EINVAL
+    assert b"max_norm" in lib.nl_last_error()
+    assert lib.nl_adamw_multi_clip(None, 0, None, 0, None, 0.9, 0.999, 1e-8, 0.1, None, 1.0) == _lib.NL_OK
+    assert lib.nl_adamw_multi_prepare(-1, None) < 0
+    # the allocation-free backward refuses sizes beyond its static scratch before any HIP call
+    S = _lib.AttnStride(64 * 4096, 64 * 4096, 64)
+    max_rows = int(re.search(r"#define NL_FLASH_BWD_NOALLOC_MAX_ROWS (\d+)", HEADER.read_text()).group(1))
+    assert lib.nl_flash_attention_bwd_noalloc(None, 1, 1, max_rows + 1, 64, 0.125, 1, 256, S, 256, S, 256, S, 256, S,
+                                              256, S, 256, 256, S, 256, S, 256, S) == _lib.NL_EINVAL
+    assert b"NL_FLASH_BWD_NOALLOC_MAX_ROWS" in lib.nl_last_error()
 
 
 def test_library_targets_gfx950_only():
