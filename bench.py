@@ -75,8 +75,15 @@ class KernelProbe:
     def tag(name, args):
         if name in ("nl_gemm", "nl_gemm_ex", "nl_gemm_fused"):
             opA, opB, M, N, K = args[1:6]
-            epi = ("", "_bias", "_bias_gelu", "_dgelu")[args[16]] if name == "nl_gemm_fused" else ""
-            return f"gemm_{'NT'[opA]}{'NT'[opB]}_{M}x{N}x{K}{epi}", 2.0 * M * N * K, "flops"
+            e = args[16] if name == "nl_gemm_fused" else 0
+            epi = ("", "_bias", "_bias_gelu", "_dgelu")[e]
+            # algorithmic bytes: bf16 operands, C at its dtype (read back too when
+            # beta != 0), the saved GELU input written (bias_gelu) or read (dgelu)
+            c_bytes = 4 if args[13] == 0 else 2
+            byt = 2.0 * (M * K + K * N) + M * N * c_bytes * (2 if args[11] != 0.0 else 1)
+            if e in (2, 3):
+                byt += 2.0 * M * N
+            return f"gemm_{'NT'[opA]}{'NT'[opB]}_{M}x{N}x{K}{epi}", 2.0 * M * N * K, "flops", byt
         if name == "nl_ce_fwd_bwd":
             M, V = args[1:3]
             return f"ce_fwd_bwd_{M}x{V}", 4.0 * M * V + 12.0 * M, "bytes"
@@ -129,21 +136,32 @@ class KernelProbe:
         return _Ctx()
 
     def summary(self, steps):
-        agg = defaultdict(lambda: [0.0, 0, 0.0, ""])
-        for (tag, work, kind), e0, e1 in self.pending:
+        agg = defaultdict(lambda: [0.0, 0, 0.0, "", None])
+        for (tag, work, kind, *byt), e0, e1 in self.pending:
             a = agg[tag]
             a[0] += e0.elapsed_time(e1) * 1e-3
             a[1] += 1
             a[2] = work
             a[3] = kind
+            a[4] = byt[0] if byt else None
         out = {}
-        for tag, (tot, n, work, kind) in agg.items():
+        for tag, (tot, n, work, kind, byt) in agg.items():
             avg = tot / n
             rate = work / avg
             if kind == "flops":
-                out[tag] = {"bound": "mfma", "achieved": rate / 1e12, "peak": PEAK_BF16_TFLOPS,
+                # the attainable roof: min(MFMA peak, arithmetic intensity x HBM
+                # bandwidth) when the algorithmic bytes are known (GEMMs)
+                peak, bound = PEAK_BF16_TFLOPS, "mfma"
+                if byt:
+                    hbm_roof = work / byt * PEAK_HBM_GBS / 1e3
+                    if hbm_roof < peak:
+                        peak, bound = hbm_roof, "hbm"
+                out[tag] = {"bound": bound, "achieved": rate / 1e12, "peak": round(peak, 1),
                             "unit": "TFLOP/s", "avg_us": avg * 1e6, "launches_per_step": n / steps,
                             "time_per_step_ms": tot / steps * 1e3, "work_per_launch": work}
+                if byt:
+                    out[tag]["bytes_per_launch"] = byt
+                    out[tag]["intensity"] = round(work / byt, 1)
             else:
                 out[tag] = {"bound": "hbm", "achieved": rate / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                             "avg_us": avg * 1e6, "launches_per_step": n / steps,
