@@ -172,20 +172,26 @@ class _LMHeadCE(torch.autograd.Function):
         loss_rows = torch.empty(M, dtype=torch.float32, device=x2.device)
         lse = torch.empty(M, dtype=torch.float32, device=x2.device)
         main = torch.cuda.current_stream(x2.device)
-        aux = wgrad._side_stream(x2.device, 1)
         n = max(1, min(int(chunks), M))
+        aux = wgrad._side_stream(x2.device, 1) if n > 1 else None
         bounds = [M * i // n for i in range(n + 1)]
         for r0, r1 in zip(bounds[:-1], bounds[1:]):
             if r1 == r0:
                 continue
             gemm_raw(x2[r0:r1], Wb, out=logits[r0:r1])
+            ce = (lambda st, r0=r0, r1=r1: _lib.call(
+                "nl_ce_fwd_bwd", st, r1 - r0, V, logits[r0].data_ptr(), ld, t[r0].data_ptr(),
+                loss_rows[r0].data_ptr(), lse[r0].data_ptr(), 1.0 / M, logits[r0].data_ptr(), ld))
+            if n == 1:
+                ce(main.cuda_stream)
+                continue
             # everything these CE launches touch was allocated above, on the
             # current stream, and stays referenced until the join below
             aux.wait_stream(main)
             with torch.cuda.stream(aux):
-                _lib.call("nl_ce_fwd_bwd", aux.cuda_stream, r1 - r0, V, logits[r0].data_ptr(), ld, t[r0].data_ptr(),
-                          loss_rows[r0].data_ptr(), lse[r0].data_ptr(), 1.0 / M, logits[r0].data_ptr(), ld)
-        main.wait_stream(aux)
+                ce(aux.cuda_stream)
+        if n > 1:
+            main.wait_stream(aux)
         ctx.save_for_backward(x2, W)
         ctx.wb = Wb
         ctx.d = logits

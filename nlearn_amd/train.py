@@ -58,8 +58,9 @@ GRAD_CLIP = float(os.environ.get("NLEARN_GRAD_CLIP", "0"))
 # NLEARN_FUSED_LMHEAD=1 fuses the LM head and the CE (linear_cross_entropy) so
 # that the (bs*seq, vocab) logits are never materialised (train.py:24-28).
 FUSED_LMHEAD = os.environ.get("NLEARN_FUSED_LMHEAD") == "1"
-# row chunks of the LM head + CE on the default path (1: one GEMM, then one CE)
-LMHEAD_CHUNKS = int(os.environ.get("NLEARN_LMHEAD_CHUNKS", "4"))
+# row chunks of the LM head + CE on the default path (1: one GEMM, then one CE;
+# more: each chunk's CE beside the next chunk's GEMM, identical results)
+LMHEAD_CHUNKS = int(os.environ.get("NLEARN_LMHEAD_CHUNKS", "1"))
 
 
 def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_lmhead: bool | None = None) -> torch.Tensor:
@@ -77,8 +78,8 @@ def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_l
     if FUSED_LMHEAD if fused_lmhead is None else fused_lmhead:
         x = model_forward_features(params, input_ids, cfg)
         return linear_cross_entropy(x.reshape(-1, cfg.d_model), output_projection(params), target_ids.reshape(-1))
-    # logits = x . W_lm and the CE in LMHEAD_CHUNKS row chunks, each chunk's
-    # CE beside the next chunk's GEMM; the same values as
+    # logits = x . W_lm and the single-pass CE (dlogits over the logits), in
+    # LMHEAD_CHUNKS row chunks; the same values as
     # cross_entropy(model_forward(...), targets, inplace=True)
     x = model_forward_features(params, input_ids, cfg)
     return lm_head_cross_entropy(x, output_projection(params), target_ids, LMHEAD_CHUNKS)
