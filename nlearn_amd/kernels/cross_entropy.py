@@ -152,12 +152,13 @@ def cross_entropy(logits: torch.Tensor, targets: torch.Tensor, inplace: bool = F
 
 
 class _LMHeadCE(torch.autograd.Function):
-    """logits = X . W in row chunks; each chunk's single CE pass (loss, lse and
-    dlogits written over the logits) runs on a second stream while the GEMM
-    computes the next chunk, so the HBM-bound CE hides behind the MFMA-bound
-    GEMM. Rows are independent in both kernels, and the CE scale is 1/M of
-    all rows, so every value equals the unchunked linear + cross_entropy bit
-    for bit. The backward is linear's, from dlogits scaled by the cotangent."""
+    """logits = X . W, then the single CE pass (loss, lse and dlogits written
+    over the logits), in row chunks. With more than one chunk, each chunk's CE
+    runs on a second stream while the GEMM computes the next chunk, so the
+    HBM-bound CE overlaps the MFMA-bound GEMM. Rows are independent in both
+    kernels, and the CE scale is 1/M of all rows, so every value equals the
+    unchunked linear + cross_entropy bit for bit. The backward is linear's,
+    from dlogits scaled by the cotangent."""
 
     @staticmethod
     def forward(ctx, x2, W, targets, chunks):
@@ -195,7 +196,6 @@ class _LMHeadCE(torch.autograd.Function):
         ctx.save_for_backward(x2, W)
         ctx.wb = Wb
         ctx.d = logits
-        ctx.mark_non_differentiable(lse)
         return mean(loss_rows)
 
     @staticmethod
@@ -208,7 +208,7 @@ class _LMHeadCE(torch.autograd.Function):
         return dx, dW, None, None
 
 
-def lm_head_cross_entropy(X: torch.Tensor, W: torch.Tensor, targets: torch.Tensor, chunks: int = 4) -> torch.Tensor:
+def lm_head_cross_entropy(X: torch.Tensor, W: torch.Tensor, targets: torch.Tensor, chunks: int = 1) -> torch.Tensor:
     """Mean CE of logits = X . W (X [..., d] bf16, W [d, V]) against ``targets``,
     equal to ``cross_entropy(linear(X, W), targets, inplace=True)`` bit for
     bit; with ``chunks`` > 1 row chunks, the CE of one chunk overlaps the GEMM
