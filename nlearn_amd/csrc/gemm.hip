@@ -19,9 +19,10 @@
 //     the weight gradient X^T.dY) stays [k][row] as in memory and is read with
 //     ds_read_b64_tr_b16, the gfx950 transposing LDS read. Nothing is ever
 //     transposed in HBM or in registers.
-//   * Double-buffered LDS stages of 64 k (both operands k-major) or 32 k
-//     (otherwise: 32 KB per workgroup, more workgroups per CU to cover L2-miss
-//     latency), one barrier per stage.
+//   * Double-buffered LDS stages of 64 k, one barrier per stage. A k-contiguous
+//     operand then arrives in 128-byte pieces of each row: when the previous
+//     kernel has just written it, it comes from DRAM, where 64-byte pieces
+//     (32-k stages) ran a third slower.
 //   * Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of
 //     tiles in groups of 8 M-tiles, sharing A and B panels in its L2.
 //   * Small outputs with a long reduction (weight gradients) split K across
@@ -385,7 +386,7 @@ __device__ __forceinline__ void wait_stage(int later) {
 
 template <int BM, int BN, int BKT, int S, bool A_KMAJ, bool B_KMAJ, typename OutT, int EPI>
 __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
-                             (BM * BN >= 65536) ? 1 : (BM == 128 && BN == 128 && BKT == 32) ? 3 : 2) void gemm2_kernel(GemmArgs g) {
+                             (BM * BN >= 65536) ? 1 : 2) void gemm2_kernel(GemmArgs g) {
   // 256 x 256 tiles run 8 waves (2 x 4), the others 4 (2 x 2); every wave
   // owns a WTM x 64 block of the tile.
   constexpr bool kHuge = BM * BN >= 65536;
@@ -1049,13 +1050,8 @@ __global__ __launch_bounds__(512, 1) void gemm_persist_kernel(GemmArgs g) {
 }
 
 // Explicit instantiations: every (layout, output, epilogue) combination the
-// dispatcher can launch gets its host stub emitted. k-stage depth per layout:
-// 64 when both operands have the same major order (NT, TN), else 32 (see launch_cfg).
-#ifndef NL_GEMM_STAGES32
-#define NL_GEMM_STAGES32 2
-#endif
-#define NL_I(AK, BKM, T, E) \
-  template __global__ void gemm2_kernel<128, 128, (AK == BKM) ? 64 : 32, (AK == BKM) ? 2 : NL_GEMM_STAGES32, AK, BKM, T, E>(GemmArgs);
+// dispatcher can launch gets its host stub emitted.
+#define NL_I(AK, BKM, T, E) template __global__ void gemm2_kernel<128, 128, 64, 2, AK, BKM, T, E>(GemmArgs);
 #define NL_I4(T, E) NL_I(true, false, T, E) NL_I(true, true, T, E) NL_I(false, false, T, E) NL_I(false, true, T, E)
 #define NL_I8(E) NL_I4(float, E) NL_I4(uint16_t, E)
 NL_I8(NL_EPI_NONE)
@@ -1204,9 +1200,12 @@ template <bool AK, bool BK_, typename OutT>
 void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
   g.tiles = p.tiles;
   g.k_chunk = p.k_chunk;
-  // Pipeline choice measured on MI355X at the model's shapes: with both
-  // operands in the same major order (NT, TN) 64-k stages win; for NN 32-k
-  // stages (32 KB of LDS, more workgroups per CU to cover L2-miss latency) win.
+  // Pipeline: two 64-k stages for every layout. For NN, 32-k stages (half the
+  // LDS, more workgroups per CU) are within a few percent when the operands
+  // sit in the last-level cache, but an operand that the previous kernel has
+  // just written comes from DRAM, and 64-byte row pieces read it a third
+  // slower than 128-byte ones (FFN-down 16384 x 512 x 2048 on a cold input:
+  // 66 -> 58 us; in the training step 52-59 -> 42-47 us).
   auto launch2 = [&](int grid) {
     if constexpr (AK || !BK_) {
       if (p.big == 2) {
@@ -1228,8 +1227,7 @@ void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
         return;
       }
     }
-    constexpr int BKT = (AK == BK_) ? 64 : 32;
-    constexpr int NS = (AK == BK_) ? 2 : NL_GEMM_STAGES32;
+    constexpr int BKT = 64, NS = 2;
     // with split K the epilogue runs in the reduction kernel
     const int epi = g.ws ? NL_EPI_NONE : g.epi;
     switch (epi) {
