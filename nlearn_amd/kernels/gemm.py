@@ -77,8 +77,15 @@ def padded_empty(rows: int, cols: int, dtype=_BF16, device="cuda") -> torch.Tens
     Wide rows (>= 1024 columns) are rounded up to 64 elements instead, so every
     row starts on a 128-byte cache line: the GEMM epilogue then writes whole
     lines (the LM-head logits with ld 50264 cost ~30% extra HBM write traffic
-    in partial lines, measured with the WRITE_SIZE counter)."""
+    in partial lines, measured with the WRITE_SIZE counter).
+
+    A stride that is a multiple of 1024 elements gets 64 more: with the
+    2048-wide FFN activations at ld 2112 instead of 2048 the bs32 x seq512
+    training step ran 0.25% faster (A/B over three rounds on one MI355X;
+    ld 2176 made no difference)."""
     ld = (cols + 7) // 8 * 8 if cols < 1024 else (cols + 63) // 64 * 64
+    if ld % 1024 == 0:
+        ld += 64
     return torch.empty((rows, ld), dtype=dtype, device=device)[:, :cols]
 
 

@@ -19,3 +19,16 @@ def test_kernel_ready_copies_overlapping_rows():
     assert _kernel_ready(d).data_ptr() == d.data_ptr() and _ld(d) == 16
     one = torch.zeros((1, 12), dtype=torch.bfloat16)
     assert _ld(one) == 16
+
+
+def test_padded_empty_row_strides():
+    """Rows start on 16-byte boundaries; rows of 1024 columns or more on
+    128-byte lines, and a stride that is a multiple of 1024 elements gets 64 more."""
+    import torch
+    from nlearn_amd.kernels.gemm import padded_empty
+
+    cases = {(3, 12): 16, (3, 512): 512, (3, 1000): 1000, (3, 1536): 1536, (3, 2048): 2112, (3, 4096): 4160,
+             (3, 2040): 2112, (3, 50257): 50304}
+    for (r, c), ld in cases.items():
+        t = padded_empty(r, c, torch.bfloat16, "cpu")
+        assert t.shape == (r, c) and t.stride() == (ld, 1), (c, t.stride())
