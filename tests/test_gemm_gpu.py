@@ -210,3 +210,31 @@ def test_gemm_tall_tile_path_exact_small_integers(dev, opA, M, N, K):
     rows = np.unique(np.concatenate([np.arange(0, 130), np.arange(M - 130, M), rng.integers(0, M, 200)]))
     got = C[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
     assert np.array_equal(got, A[rows] @ B)
+
+
+@pytest.mark.parametrize("opB,M,N,K,out", [("N", 4100, 4000, 128, "f32"), ("N", 4100, 4000, 256, "bf16"),
+                                           ("T", 4097, 4033, 384, "f32"), ("T", 16384, 2048, 512, "bf16"),
+                                           ("N", 16384, 1536, 512, "bf16")])
+def test_gemm_persistent_128_path_exact_small_integers(dev, opB, M, N, K, out):
+    """Short-K NN / NT products without an epilogue and with at least 4 tiles
+    of 128 x 128 per workgroup (two per CU) run the persistent 128 x 128
+    kernel: interior and ragged edge tiles, fp32 and bf16 outputs, checked
+    exactly on integer inputs over sampled rows including both edges."""
+    import torch
+    from nlearn_amd.kernels.gemm import gemm_raw
+
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    assert K % 128 == 0 and ((M + 127) // 128) * ((N + 127) // 128) >= 4 * cus
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-2, 3, (M, K)).astype(np.float32)
+    B = rng.integers(-2, 3, (K, N)).astype(np.float32)
+    Bs = B.T.copy() if opB == "T" else B
+    dt = torch.float32 if out == "f32" else torch.bfloat16
+    C = gemm_raw(_dev_bf16(A, dev), _dev_bf16(Bs, dev), "N", opB, out_dtype=dt)
+    torch.cuda.synchronize()
+    rows = np.unique(np.concatenate([np.arange(0, 130), np.arange(M - 130, M), rng.integers(0, M, 200)]))
+    got = C[torch.from_numpy(rows).to(dev)].float().cpu().numpy()
+    ref = A[rows] @ B
+    if out == "bf16":
+        ref = torch.from_numpy(ref).bfloat16().float().numpy()
+    assert np.array_equal(got, ref)
