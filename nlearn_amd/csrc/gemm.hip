@@ -856,19 +856,24 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
 }
 
 // ---------------------------------------------------------------------------
-// Persistent kernel for short-K products without a split or epilogue: 256 x 256
-// tiles for the LM-head forward (K = 512: 8 stages per tile, where a tile's
+// Persistent kernel for short-K products without a split: 256 x 256 tiles
+// for the LM-head forward (K = 512: 8 stages per tile, where a tile's
 // first-stage load and its 128 KB store were 30% of its time), 128 x 128 tiles
-// for smaller products with at least 4 tiles per workgroup. Each workgroup (one
-// per CU, or two with 128 x 128 tiles) walks its tiles in order. While a tile's last stage is computed, the next tile's first
-// stage is already loading into the other buffer; the tile's stores then drain
-// while the next tile computes. On gfx9 stores count in vmcnt, so the next
+// for smaller products with at least 4 tiles per workgroup, with no epilogue,
+// the bias one or the bias + GELU one (u to aux, gelu(u) to C). Each workgroup
+// (one per CU, or two with 128 x 128 tiles) walks its tiles in order. While a
+// tile's last stage is computed, the next tile's first stage is already
+// loading into the other buffer; the tile's stores then drain while the next
+// tile computes. On gfx9 stores count in vmcnt, so the next
 // tile's first wait is vmcnt(number of stores just issued): exact for interior
 // tiles, whose store path has no bounds branches; after an edge tile it is
 // vmcnt(0). Requires K % 128 == 0 (an even number of full stages, no tail).
 // ---------------------------------------------------------------------------
-template <bool A_KMAJ, bool B_KMAJ, typename OutT, int BM = 256, int BN = 256, int NWV = 8>
+template <bool A_KMAJ, bool B_KMAJ, typename OutT, int BM = 256, int BN = 256, int NWV = 8, int EPI = NL_EPI_NONE>
 __global__ __launch_bounds__(NWV * 64, NWV == 8 ? 1 : 2) void gemm_persist_kernel(GemmArgs g) {
+  static_assert(EPI == NL_EPI_NONE || EPI == NL_EPI_BIAS || EPI == NL_EPI_BIAS_GELU, "epilogues of the persistent kernel");
+  static_assert(EPI != NL_EPI_BIAS_GELU || sizeof(OutT) == 2, "the GELU epilogue writes bf16");
+  constexpr bool kBias = EPI != NL_EPI_NONE;
   // 256 x 256 tiles: 8 waves of 128 x 64, one workgroup per CU; 128 x 128
   // tiles: 4 waves of 64 x 64, two workgroups per CU
   constexpr int BKT = 64;
@@ -957,9 +962,29 @@ __global__ __launch_bounds__(NWV * 64, NWV == 8 ? 1 : 2) void gemm_persist_kerne
   constexpr int CPR = PITCH / 16;
   constexpr int EPC = 16 / (int)sizeof(OutT);
   constexpr int RPI = 64 / CPR;
-  constexpr int kStores = FM * (32 / RPI);  // store instructions per wave, interior tile
+  // store instructions per wave, interior tile (the GELU epilogue stores u and gelu(u))
+  constexpr int kStores = FM * (32 / RPI) * (EPI == NL_EPI_BIAS_GELU ? 2 : 1);
   static_assert(NWV * 32 * PITCH <= STAGE * 2, "slabs fit one stage buffer");
   static_assert(kStores < 64, "vmcnt range");
+  // the bias of the lane's columns wn*WTN + j*32 + q*8 + g4 + 0..3, loaded at
+  // the start of each tile (complete before its epilogue: later waits cover it)
+  f32x4 bias_r[kBias ? FN : 1][4];
+  auto load_bias = [&](int nb) {
+    if constexpr (kBias) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int n = nb + wn * WTN + j * 32 + q * 8 + ((lane >> 5) * 4);
+          if (n + 4 <= g.N) {
+            bias_r[j][q] = *reinterpret_cast<const f32x4*>(g.bias + n);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bias_r[j][q][e] = n + e < g.N ? g.bias[n + e] : 0.f;
+          }
+        }
+    }
+  };
   const int frow = lane & 31;
   const int g4 = (lane >> 5) * 4;
   uint8_t* wl = reinterpret_cast<uint8_t*>(st1) + wave * (32 * PITCH);
@@ -984,6 +1009,7 @@ __global__ __launch_bounds__(NWV * 64, NWV == 8 ? 1 : 2) void gemm_persist_kerne
       if (kt == 0 && pend_stores) wait_vm<kStores>();
       else wait_vm<0>();
       barrier();
+      if (kt == 0) load_bias(n0);
       issue(st1, kt * BKT + BKT);
       compute(st0);
       wait_vm<0>();
@@ -1003,46 +1029,76 @@ __global__ __launch_bounds__(NWV * 64, NWV == 8 ? 1 : 2) void gemm_persist_kerne
     __builtin_amdgcn_s_waitcnt((63 & 15) | ((63 >> 4) << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
     barrier();
     const bool interior = m0 + BM <= g.M && n0 + BN <= g.N;
+    // slab row r, 16-byte chunk ch -> rows of the output at base (ld)
+    auto copy_slab = [&](int i, auto tag, void* base, int64_t ld) __attribute__((always_inline)) {
+      using T = decltype(tag);
+      constexpr int P = 64 * (int)sizeof(T), CP = P / 16, EC = 16 / (int)sizeof(T), RI = 64 / CP;
+#pragma unroll
+      for (int it = 0; it < 32 / RI; ++it) {
+        const int r = it * RI + lane / CP;
+        const int ch = lane % CP;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(wl + r * P + ((ch ^ (r & (CP - 1))) << 4));
+        const int mm = m0 + wm * WTM + i * 32 + r;
+        const int n = n0 + wn * WTN + ch * EC;
+        T* dst = reinterpret_cast<T*>(base) + (int64_t)mm * ld + n;
+        if (interior) {
+          __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+        } else {
+          if (mm >= g.M || n >= g.N) continue;
+          if (n + EC <= g.N) {
+            __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
+          } else {
+#pragma unroll
+            for (int k = 0; k < EC; ++k) {
+              if (n + k >= g.N) break;
+              if constexpr (sizeof(T) == 2) dst[k] = (T)(val[k >> 1] >> (16 * (k & 1)));
+              else dst[k] = __uint_as_float(val[k]);
+            }
+          }
+        }
+      }
+    };
+    auto slab_bf16 = [&](int j, int q) {
+      const int c = j * 32 + q * 8 + g4;
+      return reinterpret_cast<u32x2*>(wl + frow * 128 + ((((c * 2) >> 4) ^ (frow & 7)) << 4) + ((c * 2) & 15));
+    };
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int j = 0; j < FN; ++j)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const float x0 = acc[i][j][4 * q] * s, x1 = acc[i][j][4 * q + 1] * s, x2 = acc[i][j][4 * q + 2] * s,
-                      x3 = acc[i][j][4 * q + 3] * s;
+          float x[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[e] = acc[i][j][4 * q + e] * s;
+            if constexpr (kBias) x[e] += bias_r[j][q][e];
+          }
           const int c = j * 32 + q * 8 + g4;
           if constexpr (sizeof(OutT) == 2) {
-            *reinterpret_cast<u32x2*>(wl + frow * 128 + ((((c * 2) >> 4) ^ (frow & 7)) << 4) + ((c * 2) & 15)) =
-                u32x2{pack_bf16x2(x0, x1), pack_bf16x2(x2, x3)};
+            *slab_bf16(j, q) = u32x2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
           } else {
-            *reinterpret_cast<f32x4*>(wl + frow * 256 + ((((c * 4) >> 4) ^ (frow & 15)) << 4)) = f32x4{x0, x1, x2, x3};
+            *reinterpret_cast<f32x4*>(wl + frow * 256 + ((((c * 4) >> 4) ^ (frow & 15)) << 4)) =
+                f32x4{x[0], x[1], x[2], x[3]};
           }
         }
+      if constexpr (EPI == NL_EPI_BIAS_GELU) {
+        // the pre-activation u = bf16(v + bias) goes to aux; then C = gelu(u)
+        // from the lane's own slab entries
+        copy_slab(i, uint16_t{}, g.aux, g.ldaux);
+        u32x2 uu[FN][4];
 #pragma unroll
-      for (int it = 0; it < 32 / RPI; ++it) {
-        const int r = it * RPI + lane / CPR;
-        const int ch = lane % CPR;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(wl + r * PITCH + ((ch ^ (r & (CPR - 1))) << 4));
-        const int mm = m0 + wm * WTM + i * 32 + r;
-        const int n = n0 + wn * WTN + ch * EPC;
-        OutT* dst = reinterpret_cast<OutT*>(g.C) + (int64_t)mm * g.ldc + n;
-        if (interior) {
-          __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
-        } else {
-          if (mm >= g.M || n >= g.N) continue;
-          if (n + EPC <= g.N) {
-            __builtin_nontemporal_store(val, reinterpret_cast<u32x4*>(dst));
-          } else {
+        for (int j = 0; j < FN; ++j)
 #pragma unroll
-            for (int k = 0; k < EPC; ++k) {
-              if (n + k >= g.N) break;
-              if constexpr (sizeof(OutT) == 2) dst[k] = (OutT)(val[k >> 1] >> (16 * (k & 1)));
-              else dst[k] = __uint_as_float(val[k]);
-            }
-          }
-        }
+          for (int q = 0; q < 4; ++q) uu[j][q] = *slab_bf16(j, q);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *slab_bf16(j, q) = u32x2{pack_bf16x2(gelu_tanh(bf16_lo(uu[j][q][0])), gelu_tanh(bf16_hi(uu[j][q][0]))),
+                                     pack_bf16x2(gelu_tanh(bf16_lo(uu[j][q][1])), gelu_tanh(bf16_hi(uu[j][q][1])))};
       }
+      copy_slab(i, OutT{}, g.C, g.ldc);
     }
     if (!has_next) break;
     pend_stores = interior;
@@ -1075,6 +1131,12 @@ template __global__ void gemm_persist_kernel<true, false, float, 128, 128, 4>(Ge
 template __global__ void gemm_persist_kernel<true, false, uint16_t, 128, 128, 4>(GemmArgs);
 template __global__ void gemm_persist_kernel<true, true, float, 128, 128, 4>(GemmArgs);
 template __global__ void gemm_persist_kernel<true, true, uint16_t, 128, 128, 4>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, false, float, 128, 128, 4, NL_EPI_BIAS>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, false, uint16_t, 128, 128, 4, NL_EPI_BIAS>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, true, float, 128, 128, 4, NL_EPI_BIAS>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, true, uint16_t, 128, 128, 4, NL_EPI_BIAS>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, false, uint16_t, 128, 128, 4, NL_EPI_BIAS_GELU>(GemmArgs);
+template __global__ void gemm_persist_kernel<true, true, uint16_t, 128, 128, 4, NL_EPI_BIAS_GELU>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, true, uint16_t, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, float, NL_EPI_NONE>(GemmArgs);
 template __global__ void gemm2_kernel<256, 256, 64, 2, true, false, uint16_t, NL_EPI_NONE>(GemmArgs);
@@ -1235,18 +1297,29 @@ void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
       }
     }
     constexpr int BKT = 64, NS = 2;
-    // Short-K products with at least 4 tiles per workgroup and no epilogue
-    // (the QKV projection): the persistent kernel, two 128 x 128 workgroups
-    // per CU, each loading its next tile's first stage under its current
-    // tile's last one. Measured at 16384 x 1536 x 512: 37 -> 34 us (operands
-    // in the caches), 42 -> 40 us (flushed first).
+    // Short-K products with at least 4 tiles per workgroup and no epilogue or a
+    // bias / bias + GELU one (QKV and FFN-up): the persistent kernel, two
+    // 128 x 128 workgroups per CU, each loading its next tile's first stage
+    // under its current tile's last one and storing a tile while computing the
+    // next. Measured at 16384 x 1536 x 512: 37 -> 34 us (operands in the
+    // caches), 42 -> 40 us (flushed first).
     if constexpr (AK) {
-      if (!g.ws && g.beta == 0.f && g.epi == NL_EPI_NONE && g.K % 128 == 0 && g.K <= 4096) {
+      const bool epi_ok = g.epi == NL_EPI_NONE || g.epi == NL_EPI_BIAS ||
+                          (g.epi == NL_EPI_BIAS_GELU && sizeof(OutT) == 2);
+      if (!g.ws && g.beta == 0.f && epi_ok && g.K % 128 == 0 && g.K <= 4096) {
         const int cus = cu_count();
         const int ntiles = (int)((int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128));
         if (ntiles >= 4 * cus) {
-          hipLaunchKernelGGL((gemm_persist_kernel<AK, BK_, OutT, 128, 128, 4>), dim3(std::max(8, cus * 2 / 8 * 8)),
-                             dim3(256), 0, st, g);
+          const dim3 grid(std::max(8, cus * 2 / 8 * 8)), block(256);
+          if (g.epi == NL_EPI_BIAS) {
+            hipLaunchKernelGGL((gemm_persist_kernel<AK, BK_, OutT, 128, 128, 4, NL_EPI_BIAS>), grid, block, 0, st, g);
+          } else if (g.epi == NL_EPI_BIAS_GELU) {
+            if constexpr (sizeof(OutT) == 2)
+              hipLaunchKernelGGL((gemm_persist_kernel<AK, BK_, OutT, 128, 128, 4, NL_EPI_BIAS_GELU>), grid, block, 0,
+                                 st, g);
+          } else {
+            hipLaunchKernelGGL((gemm_persist_kernel<AK, BK_, OutT, 128, 128, 4>), grid, block, 0, st, g);
+          }
           return;
         }
       }
