@@ -1306,7 +1306,8 @@ void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
     if constexpr (AK) {
       const bool epi_ok = g.epi == NL_EPI_NONE || g.epi == NL_EPI_BIAS ||
                           (g.epi == NL_EPI_BIAS_GELU && sizeof(OutT) == 2);
-      if (!g.ws && g.beta == 0.f && epi_ok && g.K % 128 == 0 && g.K <= 4096) {
+      // (K = 0 stays on gemm2_kernel, which issues no DMA then: A and B may be null)
+      if (!g.ws && g.beta == 0.f && epi_ok && g.K >= 128 && g.K % 128 == 0 && g.K <= 4096) {
         const int cus = cu_count();
         const int ntiles = (int)((int64_t)((g.M + 127) / 128) * ((g.N + 127) / 128));
         if (ntiles >= 4 * cus) {

@@ -228,3 +228,36 @@ def test_gemm_nt_n_panels_beyond_2gb(dev, big):
     cols = sorted(set(EDGE) | set(rng.integers(0, BIG_ROWS, 12).tolist()))
     ref = Ah @ _rows_of(big, cols).T
     assert np.array_equal(_np(C)[:, cols].astype(np.float64), ref)
+
+
+@pytest.mark.parametrize("epi", ["none", "bias", "bias_gelu"])
+def test_gemm_k_zero_large_output(dev, epi):
+    """K = 0 with null A and B over an output of more than 1024 tiles of
+    128 x 128 (the size the persistent short-K kernel takes for K >= 128):
+    C = epilogue(0), with no operand read."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_NONE
+    from oracle import model_np as om
+
+    M, N = 4100, 4000
+    C = torch.full((M, N), 7.0, dtype=torch.bfloat16, device=dev)
+    bias = torch.arange(N, dtype=torch.float32, device=dev) / 8
+    aux = torch.full((M, N), 5.0, dtype=torch.bfloat16, device=dev)
+    code = {"none": EPI_NONE, "bias": EPI_BIAS, "bias_gelu": EPI_BIAS_GELU}[epi]
+    st = torch.cuda.current_stream().cuda_stream
+    _lib.call("nl_gemm_fused", st, _lib.NL_OP_N, _lib.NL_OP_N, M, N, 0, 1.0, None, 8, None, N, 0.0,
+              C.data_ptr(), _lib.NL_DTYPE_BF16, N, None, code,
+              bias.data_ptr() if epi != "none" else None, aux.data_ptr() if epi == "bias_gelu" else None,
+              N if epi == "bias_gelu" else 0, None, 0)
+    torch.cuda.synchronize()
+    if epi == "none":
+        assert torch.count_nonzero(C).item() == 0
+        return
+    u = bias.to(torch.bfloat16).expand(M, N)
+    if epi == "bias":
+        assert torch.equal(C, u)
+    else:
+        assert torch.equal(aux, u)
+        ref = om._gelu(_np(u).astype(np.float64))[0]
+        assert np.abs(_np(C) - ref).max() <= np.abs(ref).max() * 2 ** -8 + 1e-6
