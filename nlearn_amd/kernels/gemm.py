@@ -84,7 +84,7 @@ def padded_empty(rows: int, cols: int, dtype=_BF16, device="cuda") -> torch.Tens
     training step ran 0.25% faster (A/B over three rounds on one MI355X;
     ld 2176 made no difference)."""
     ld = (cols + 7) // 8 * 8 if cols < 1024 else (cols + 63) // 64 * 64
-    if ld % 1024 == 0:
+    if ld >= 1024 and ld % 1024 == 0:
         ld += 64
     return torch.empty((rows, ld), dtype=dtype, device=device)[:, :cols]
 
