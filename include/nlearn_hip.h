@@ -435,12 +435,19 @@ int nl_colsum_bf16(void* stream, int rows, int cols, const nl_bf16* x, int64_t l
 int nl_embedding_fwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
                      const float* tok, const float* pos, nl_bf16* out);
 
-/* dtok[ids[t]] += dx[t] (fp32 atomics: the caller zeroes dtok; repeated ids are
- * summed in hardware order), dpos[s] (+)= sum_b dx[b][s] in batch order for
- * s < seq (rows of dpos at or past seq are not touched). One kernel launch.
+/* dtok[v] = sum of dx[t] over the tokens t with ids[t] == v, in increasing t
+ * (deterministic, no atomics: np.add.at's order), for every row v of the
+ * [vocab][D] table: rows no token uses are written as zero, so dtok needs no
+ * zeroing first. dpos[s] (+)= sum_b dx[b][s] in batch order for s < seq (rows of
+ * dpos at or past seq are not touched). D % 4 == 0, D <= 4096; dtok 16-byte and
+ * dx 8-byte aligned. Two launches (the positions of each vocabulary bucket
+ * listed in token order, then the rows) over a workspace of
+ * nl_embedding_bwd_ws_bytes() bytes, 16-byte aligned (unused with no tokens).
  * The autodiff of the gather in model.py:75-85. */
+size_t nl_embedding_bwd_ws_bytes(int batch, int seq, int D, int vocab);
 int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
-                     const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos);
+                     const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos, void* ws,
+                     size_t ws_bytes);
 
 #ifdef __cplusplus
 }

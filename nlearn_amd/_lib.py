@@ -88,7 +88,8 @@ _SIGNATURES = {
     "nl_colsum_ws_bytes": [_I, _I],
     "nl_colsum_bf16": [_P, _I, _I, _P, _I64, _P, _I, _P, ctypes.c_size_t],
     "nl_embedding_fwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
-    "nl_embedding_bwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I],
+    "nl_embedding_bwd_ws_bytes": [_I, _I, _I, _I],
+    "nl_embedding_bwd": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _I, _P, ctypes.c_size_t],
 }
 _RESTYPES = {
     "nl_strerror": ctypes.c_char_p,
@@ -101,6 +102,7 @@ _RESTYPES = {
     "nl_colsum_ws_bytes": ctypes.c_size_t,
     "nl_lce_ws_bytes": ctypes.c_size_t,
     "nl_global_norm_ws_bytes": ctypes.c_size_t,
+    "nl_embedding_bwd_ws_bytes": ctypes.c_size_t,
 }
 
 EXPORTED = tuple(_SIGNATURES)

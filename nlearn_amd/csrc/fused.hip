@@ -358,17 +358,107 @@ __global__ __launch_bounds__(128) void embed_fwd_kernel(int S, int D, const int3
   }
 }
 
-// One launch for both tables. Workgroups [0, S) form dpos[s] (+)= sum_b dx[b, s]
-// in batch order (launched first: each reads B rows); workgroups [S, S + B*S)
-// add dx[t] into dtok[ids[t]] with fp32 atomics (rows of repeated tokens are
-// summed in hardware order, the one non-deterministic sum of the step); ids
-// outside [0, vocab) contribute nothing.
-__global__ __launch_bounds__(128) void embed_bwd_kernel(int B, int S, int D, const int32_t* __restrict__ ids,
-                                                        const uint16_t* __restrict__ dx, float* __restrict__ dtok,
-                                                        int vocab, float* __restrict__ dpos, int accumulate) {
+// The embedding backward, deterministic and without atomics, in two launches.
+//
+// embed_bucket_kernel: workgroup (b, k) owns the vocabulary rows
+// [b W, b W + W) (a bucket) and the k-th of P equal ranges of token positions.
+// It scans its range in order, appending (t, ids[t]) for the positions whose
+// id falls in its rows to its own segment lists[b][k][0, counts[b][k])
+// (capacity the range's length), so each segment is in increasing t and the
+// segments of a bucket in order are too. Ids outside [0, vocab) go nowhere.
+//
+// embed_bwd_kernel (one wave per workgroup):
+// * workgroups [0, S) form dpos[s] (+)= sum_b dx[b, s] in batch order;
+// * workgroup S + g owns the token-table rows [g R, g R + R) (R divides W) in
+//   LDS, walks its bucket's segments in order and adds dx[t] to row ids[t] for the
+//   positions whose id it owns: each (row, column) is summed by one lane in
+//   increasing t (np.add.at's order). Every owned row is then written, zero when
+//   no token has its id, so dtok needs no zeroing first.
+constexpr int kEmbTokLds = 16384;  // bytes of LDS per row workgroup (R = 16384 / (4 D) rows)
+constexpr int kEmbBuckets = 256;   // target number of buckets
+constexpr int kEmbParts = 4;       // token ranges per bucket (one scanning workgroup each)
+
+struct EmbPlan {
+  int R;        // token-table rows per row workgroup
+  int W;        // rows per bucket, a multiple of R
+  int buckets;  // ceil(vocab / W)
+  int64_t groups;
+};
+EmbPlan emb_plan(int D, int vocab) {
+  EmbPlan p;
+  p.R = std::max(1, kEmbTokLds / (D * 4));
+  const int want = (vocab + kEmbBuckets - 1) / kEmbBuckets;
+  p.W = (want + p.R - 1) / p.R * p.R;
+  p.buckets = (vocab + p.W - 1) / p.W;
+  p.groups = ((int64_t)vocab + p.R - 1) / p.R;
+  return p;
+}
+
+__global__ __launch_bounds__(256) void embed_bucket_kernel(int T, int vocab, int W, const int32_t* __restrict__ ids,
+                                                           int* __restrict__ counts, int2* __restrict__ lists) {
+  __shared__ int wave_tot[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x / kEmbParts, k_part = blockIdx.x % kEmbParts;
+  const int v0 = b * W;
+  const int nrows = min(W, vocab - v0);
+  const int span = (T + kEmbParts - 1) / kEmbParts;
+  const int t0 = k_part * span, t1 = min(T, t0 + span);
+  int2* list = lists + (int64_t)b * T + t0;  // the segment: span entries from t0
+  int cursor = 0;
+  // thread tid holds positions c0 + 4 tid + e: in t order thread by thread, e
+  // within; the next chunk's ids are loaded before this chunk is placed
+  int cur[4], nxt[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) cur[e] = t0 + 4 * tid + e < t1 ? ids[t0 + 4 * tid + e] : -1;
+  for (int c0 = t0; c0 < t1; c0 += 1024) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = c0 + 1024 + 4 * tid + e;
+      nxt[e] = t < t1 ? ids[t] : -1;
+    }
+    bool hit[4];
+    int k = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      hit[e] = (uint32_t)(cur[e] - v0) < (uint32_t)nrows;
+      k += hit[e];
+    }
+    // exclusive prefix of k over the workgroup (wave scan, then wave totals)
+    int incl = k;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += y;
+    }
+    if (lane == 63) wave_tot[wave] = incl;
+    __syncthreads();
+    int base = cursor, total = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (w < wave) base += wave_tot[w];
+      total += wave_tot[w];
+    }
+    int pos = base + incl - k;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (hit[e]) list[pos++] = int2{c0 + 4 * tid + e, cur[e]};
+    cursor += total;
+    __syncthreads();  // wave_tot is rewritten by the next chunk
+#pragma unroll
+    for (int e = 0; e < 4; ++e) cur[e] = nxt[e];
+  }
+  if (tid == 0) counts[blockIdx.x] = cursor;  // counts[b][k]
+}
+
+__global__ __launch_bounds__(64) void embed_bwd_kernel(int B, int S, int D, const int32_t* __restrict__ ids,
+                                                       const uint16_t* __restrict__ dx, float* __restrict__ dtok,
+                                                       int vocab, int R, int W, const int* __restrict__ counts,
+                                                       const int2* __restrict__ lists, float* __restrict__ dpos,
+                                                       int accumulate) {
+  const int lane = threadIdx.x;
   if ((int)blockIdx.x < S) {
     const int s = blockIdx.x;
-    for (int c = threadIdx.x; c < D; c += 128) {
+    for (int c = lane; c < D; c += 64) {
       float a = 0.f;
 #pragma unroll 8
       for (int b = 0; b < B; ++b) a += bf16_to_f32(dx[((int64_t)b * S + s) * D + c]);
@@ -377,11 +467,46 @@ __global__ __launch_bounds__(128) void embed_bwd_kernel(int B, int S, int D, con
     }
     return;
   }
-  const int t = blockIdx.x - S;
-  const int id = ids[t];
-  if (id < 0 || id >= vocab) return;
-  for (int c = threadIdx.x; c < D; c += 128)
-    atomicAdd(dtok + (int64_t)id * D + c, bf16_to_f32(dx[(int64_t)t * D + c]));
+  extern __shared__ f32x4 emb_acc4[];
+  float* acc = reinterpret_cast<float*>(emb_acc4);
+  const int T = B * S;
+  const int v0 = ((int)blockIdx.x - S) * R;
+  const int nrows = min(R, vocab - v0);
+  const int n4 = nrows * D / 4;
+  for (int i = lane; i < n4; i += 64) emb_acc4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  __syncthreads();
+  const int b = v0 / W;
+  const int span = (T + kEmbParts - 1) / kEmbParts;
+  // the bucket's segments in order: every position of segment k precedes those of k + 1
+  for (int kp = 0; kp < (T > 0 ? kEmbParts : 0); ++kp) {
+    const int n = counts[b * kEmbParts + kp];
+    const int2* list = lists + (int64_t)b * T + (int64_t)kp * span;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+      const int2 e = j0 + lane < n ? list[j0 + lane] : int2{0, -1};
+      const int t = e.x, id = e.y;
+      uint64_t hits = __ballot((uint32_t)(id - v0) < (uint32_t)nrows);
+      while (hits) {
+        const int l = __builtin_ctzll(hits);
+        hits &= hits - 1;
+        const int tl = __builtin_amdgcn_readlane(t, l);
+        const int row = __builtin_amdgcn_readlane(id, l) - v0;
+        const uint16_t* src = dx + (int64_t)tl * D;
+        float* dst = acc + row * D;
+        for (int c = lane * 4; c < D; c += 256) {
+          const u32x2 x = *reinterpret_cast<const u32x2*>(src + c);
+          f32x4 a = *reinterpret_cast<const f32x4*>(dst + c);
+          a[0] += bf16_lo(x[0]);
+          a[1] += bf16_hi(x[0]);
+          a[2] += bf16_lo(x[1]);
+          a[3] += bf16_hi(x[1]);
+          *reinterpret_cast<f32x4*>(dst + c) = a;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  f32x4* out = reinterpret_cast<f32x4*>(dtok + (int64_t)v0 * D);
+  for (int i = lane; i < n4; i += 64) out[i] = emb_acc4[i];
 }
 
 int vectors_per_lane(int D) {
@@ -578,13 +703,42 @@ extern "C" int nl_embedding_fwd(void* stream, int batch, int seq, int D, int voc
   return nl_check_launch("nl_embedding_fwd");
 }
 
+extern "C" size_t nl_embedding_bwd_ws_bytes(int batch, int seq, int D, int vocab) {
+  if (batch <= 0 || seq <= 0 || D <= 0 || vocab <= 0) return 0;
+  const EmbPlan p = emb_plan(D, vocab);
+  // counts, then 8-byte (t, id) entries from a 16-byte boundary
+  return ((size_t)p.buckets * kEmbParts * sizeof(int) + 15) / 16 * 16 + (size_t)p.buckets * batch * seq * sizeof(int2);
+}
+
 extern "C" int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
-                                const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos) {
-  if (batch < 0 || seq < 0 || D <= 0 || vocab <= 0) return nl_set_error(NL_EINVAL, "embedding_bwd: bad shape");
-  if (batch == 0 || seq == 0) return NL_OK;
-  if (!ids || !dx || !dtok || !dpos) return nl_set_error(NL_EINVAL, "embedding_bwd: null pointer");
-  if ((int64_t)batch * seq + seq > 0x7fffffff) return nl_set_error(NL_EINVAL, "embedding_bwd: too many tokens");
-  hipLaunchKernelGGL(embed_bwd_kernel, dim3(seq + batch * seq), dim3(128), 0, (hipStream_t)stream, batch, seq, D, ids,
-                     dx, dtok, vocab, dpos, accumulate_pos);
+                                const nl_bf16* dx, float* dtok, float* dpos, int accumulate_pos, void* ws,
+                                size_t ws_bytes) {
+  if (batch < 0 || seq < 0 || D <= 0 || (D % 4) != 0 || vocab <= 0)
+    return nl_set_error(NL_EINVAL, "embedding_bwd: need D % 4 == 0 and vocab > 0");
+  if (D * 4 > kEmbTokLds) return nl_set_error(NL_EINVAL, "embedding_bwd: D above 4096");
+  const int64_t T64 = (int64_t)batch * seq;
+  if (!dtok || (seq > 0 && !dpos) || (T64 > 0 && (!ids || !dx)))
+    return nl_set_error(NL_EINVAL, "embedding_bwd: null pointer");
+  if ((((uintptr_t)dtok) & 15) != 0 || (((uintptr_t)dx) & 7) != 0)
+    return nl_set_error(NL_EALIGN, "embedding_bwd: dtok must be 16-byte and dx 8-byte aligned");
+  if (T64 > 0x7fffffff - 1024) return nl_set_error(NL_EINVAL, "embedding_bwd: too many tokens");
+  const EmbPlan p = emb_plan(D, vocab);
+  if (seq + p.groups > 0x7fffffff) return nl_set_error(NL_EINVAL, "embedding_bwd: vocabulary too large");
+  const int T = (int)T64;
+  hipStream_t st = (hipStream_t)stream;
+  int* counts = nullptr;
+  int2* lists = nullptr;
+  if (T > 0) {
+    if (!ws || ws_bytes < nl_embedding_bwd_ws_bytes(batch, seq, D, vocab) || ((uintptr_t)ws & 15) != 0)
+      return nl_set_error(NL_EINVAL, "embedding_bwd: workspace below nl_embedding_bwd_ws_bytes()");
+    counts = reinterpret_cast<int*>(ws);
+    lists = reinterpret_cast<int2*>(reinterpret_cast<char*>(ws) +
+                                    ((size_t)p.buckets * kEmbParts * sizeof(int) + 15) / 16 * 16);
+    hipLaunchKernelGGL(embed_bucket_kernel, dim3(p.buckets * kEmbParts), dim3(256), 0, st, T, vocab, p.W, ids, counts,
+                       lists);
+  }
+  // with no tokens every row of dtok is still written (zero): counts is not read then
+  hipLaunchKernelGGL(embed_bwd_kernel, dim3((unsigned)(seq + p.groups)), dim3(64), p.R * D * 4, st, batch, seq, D,
+                     ids, dx, dtok, vocab, p.R, p.W, counts, lists, dpos, accumulate_pos);
   return nl_check_launch("nl_embedding_bwd");
 }

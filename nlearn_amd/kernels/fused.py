@@ -303,15 +303,18 @@ def _embedding_bwd(ids32, dx, dims, bufs):
     B, S, D, V, pshape = dims
     dx = dx.to(_BF16).contiguous()
     gt, gp = bufs
-    # zero_() is a fill kernel (no memset node when the step is captured); the
-    # kernel writes rows [0, S) of dpos, so only longer tables need one
-    dtok = gt.zero_() if gt is not None else torch.zeros((V, D), dtype=_F32, device=dx.device)
+    # the kernel writes every row of dtok (zero where no token has the id); of
+    # dpos it writes rows [0, S), so only a longer table needs a fill (zero_()
+    # is a fill kernel: no memset node when the step is captured)
+    dtok = gt if gt is not None else torch.empty((V, D), dtype=_F32, device=dx.device)
     if gp is None:
         dpos = torch.zeros(pshape, dtype=_F32, device=dx.device)
     else:
         dpos = gp.zero_() if pshape[0] > S else gp
+    wsb = int(_lib.load().nl_embedding_bwd_ws_bytes(B, S, D, V))
+    ws = torch.empty(max(wsb, 16) // 4, dtype=torch.int32, device=dx.device)
     _lib.call("nl_embedding_bwd", _stream(dx), B, S, D, V, ids32.data_ptr(), dx.data_ptr(), dtok.data_ptr(),
-              dpos.data_ptr(), 0)
+              dpos.data_ptr(), 0, ws.data_ptr(), wsb)
     return _unless_buffered(bufs, (dtok, dpos))
 
 

@@ -273,6 +273,47 @@ def test_embedding_fwd_bwd(dev, B, S, V, D, P):
     assert np.array_equal(_np(posd.grad), dpos)
 
 
+def test_embedding_bwd_sums_in_token_order(dev):
+    """Skewed ids (one id on a quarter of the tokens, a few hot ones, runs of
+    the same id) and non-integer gradients, where the summation order shows in
+    the last bits: the token table's gradient is np.add.at's float32 sum, in
+    increasing token order, bit for bit; rows no token uses come back zero in
+    a table that started as NaN; ids outside [0, vocab) add nothing."""
+    import torch
+    from nlearn_amd import _lib
+
+    B, S, V, D = 8, 1000, 3000, 512
+    rng = np.random.default_rng(11)
+    ids = rng.integers(0, V, (B, S)).astype(np.int32)
+    ids[rng.random((B, S)) < 0.25] = 17
+    ids[:, 100:140] = 2999
+    ids[3, 7] = V
+    ids[5, 9] = -4
+    dx = ops.bf16_round(rng.standard_normal((B, S, D)).astype(np.float32))
+    dtok = torch.full((V, D), float("nan"), device=dev)
+    dpos = torch.zeros((S, D), device=dev)
+    outs = []
+    wsb = int(_lib.load().nl_embedding_bwd_ws_bytes(B, S, D, V))
+    ws = torch.empty(wsb // 4, dtype=torch.int32, device=dev)
+    for _ in range(2):
+        ws.fill_(-1)                                              # stale workspace contents must not matter
+        _lib.call("nl_embedding_bwd", torch.cuda.current_stream().cuda_stream, B, S, D, V,
+                  torch.from_numpy(ids).to(dev).data_ptr(), _dev_bf16(dx, dev).data_ptr(), dtok.data_ptr(),
+                  dpos.data_ptr(), 0, ws.data_ptr(), wsb)
+        torch.cuda.synchronize()
+        outs.append(_np(dtok).copy())
+    flat, rows = ids.reshape(-1), dx.reshape(-1, D)
+    keep = (flat >= 0) & (flat < V)
+    ref = np.zeros((V, D), np.float32)
+    np.add.at(ref, flat[keep], rows[keep])
+    assert np.array_equal(outs[0], ref)
+    assert np.array_equal(outs[1], outs[0])
+    ref_pos = np.zeros((S, D), np.float32)
+    for b in range(B):                                            # batch order, as the kernel
+        ref_pos += dx[b]
+    assert np.array_equal(_np(dpos), ref_pos)
+
+
 def test_embedding_invalid_ids_give_nan_rows(dev):
     import torch
     from nlearn_amd.kernels.fused import embedding

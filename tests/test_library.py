@@ -73,6 +73,15 @@ def test_status_strings_and_argument_errors_without_gpu():
     assert lib.nl_colsum_ws_bytes(16384, 2048) == 256 * 2048 * 4
     assert lib.nl_colsum_bf16(None, 8, 8, 256, 12, 512, 0, 768, 4096) == _lib.NL_EALIGN
     assert lib.nl_embedding_fwd(None, 2, 8, 6, 100, 256, 512, 768, 1024) == _lib.NL_EINVAL
+    # embedding backward: 252 buckets of 200 rows for the LM vocabulary at D = 512, 4 counts and T positions each
+    assert lib.nl_embedding_bwd_ws_bytes(32, 512, 512, 50257) == 4032 + 252 * 16384 * 8
+    assert lib.nl_embedding_bwd_ws_bytes(0, 512, 512, 50257) == 0
+    eargs = (None, 2, 8, 512, 100, 256, 512, 768, 1024, 0)
+    assert lib.nl_embedding_bwd(*eargs, 1280, 16) == _lib.NL_EINVAL                    # workspace too small
+    assert b"workspace" in lib.nl_last_error()
+    assert lib.nl_embedding_bwd(None, 2, 8, 6, 100, 256, 512, 768, 1024, 0, None, 0) == _lib.NL_EINVAL   # D % 4
+    assert lib.nl_embedding_bwd(None, 2, 8, 8192, 100, 256, 512, 768, 1024, 0, None, 0) == _lib.NL_EINVAL
+    assert lib.nl_embedding_bwd(None, 2, 8, 512, 100, 256, 512, 776, 1024, 0, None, 0) == _lib.NL_EALIGN
     # optimizer-side entry points: accumulation, global norm, clipped update
     assert lib.nl_grad_accumulate(None, 0, None, None, None) == _lib.NL_OK            # nothing to do
     assert lib.nl_grad_accumulate(None, -1, None, None, None) == _lib.NL_EINVAL
