@@ -129,3 +129,25 @@ def test_ce_full_size_properties(dev):
     mean_loss = ce.mean(loss).item()
     # E[loss] for N(0, s^2) logits ~= ln V + s^2/2
     assert abs(mean_loss - (math.log(V) + 2.0)) < 0.05
+
+
+@pytest.mark.parametrize("rows,cols,ld,offset", [(300, 50257, 50304, 0), (7, 13, 16, 0), (9, 40, 48, 1)])
+def test_scale_by_device_scalar(dev, rows, cols, ld, offset):
+    """dlogits *= g (the CE backward's cotangent) in place: bf16(x * g) with one
+    RNE rounding per element, on 16-byte aligned rows (8 elements per load,
+    ragged tails) and on rows that start off that alignment (element path);
+    g == 1 leaves every bit, the padding included, untouched."""
+    import torch
+    from nlearn_amd.kernels.cross_entropy import scale_by_device_scalar_
+
+    gen = torch.Generator(device="cpu").manual_seed(rows + cols)
+    base = torch.randn(rows * ld + offset, generator=gen).to(torch.bfloat16).to(dev)
+    x = base[offset:].view(rows, ld)[:, :cols]
+    for g in (3.0, 1.0, -0.37):
+        before = base.clone()
+        scale_by_device_scalar_(x, torch.tensor(g, device=dev))
+        torch.cuda.synchronize()
+        want = before[offset:].view(rows, ld).clone()
+        want[:, :cols] = (want[:, :cols].float() * g).to(torch.bfloat16)
+        assert torch.equal(base[offset:].view(rows, ld), want)
+        assert torch.equal(base[:offset], before[:offset])
