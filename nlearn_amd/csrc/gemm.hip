@@ -453,11 +453,19 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
                                                 : (int64_t)(g.K - 1) * g.ldb + g.N) * 2) + 15) & ~(int64_t)15);
   const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, a_bytes);
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, b_bytes);
-  Dma<BM, BKT, A_KMAJ, NWV> da;
-  Dma<BN, BKT, B_KMAJ, NWV> db;
-  da.init(m0, g.lda, wave, lane);
-  db.init(n0, g.ldb, wave, lane);
-  constexpr int IPS = Dma<BM, BKT, A_KMAJ, NWV>::INSTR + Dma<BN, BKT, B_KMAJ, NWV>::INSTR;  // DMA ops per stage per wave
+  // The 8-wave TN tile (the LM-head weight gradient) gives each stage's DMA
+  // to half of its waves, alternating by stage (waves w and w + 4 share a
+  // SIMD). Issued by all 8 waves at once, the 64 KB queued behind a CU's
+  // ~28 B/clk global -> LDS path and blocked both waves of every SIMD for
+  // 800+ cycles per stage with the MFMA pipe idle; this way one of the two
+  // computes meanwhile. Measured at 512 x 50257 x 16384: 771-777 -> 737-744 us.
+  // (Slower for the NT form, 672-695 -> 694-708 us, and for 128 x 128 tiles.)
+  constexpr int DNW = (!A_KMAJ && !B_KMAJ && kHuge && S == 2) ? NWV / 2 : NWV;
+  Dma<BM, BKT, A_KMAJ, DNW> da;
+  Dma<BN, BKT, B_KMAJ, DNW> db;
+  da.init(m0, g.lda, wave % DNW, lane);
+  db.init(n0, g.ldb, wave % DNW, lane);
+  constexpr int IPS = Dma<BM, BKT, A_KMAJ, DNW>::INSTR + Dma<BN, BKT, B_KMAJ, DNW>::INSTR;  // DMA ops per stage per issuing wave
 
   Frag<BM, BKT, A_KMAJ> fa[FM];
   Frag<BN, BKT, B_KMAJ> fb[FN];
@@ -503,9 +511,11 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
     }
   };
   auto issue = [&](uint16_t* sb, int st) __attribute__((always_inline)) {  // DMA of stage st (0-based in this split)
-    const int k0 = kbeg + st * BKT;
-    da.issue(ra, sb, k0, g.lda, wave);
-    db.issue(rb, sb + BM * BKT, k0, g.ldb, wave);
+    if (DNW == NWV || wave / DNW == (st & 1)) {
+      const int k0 = kbeg + st * BKT;
+      da.issue(ra, sb, k0, g.lda, wave % DNW);
+      db.issue(rb, sb + BM * BKT, k0, g.ldb, wave % DNW);
+    }
   };
 
   // S-stage pipeline, unrolled by S so that every buffer is a fixed LDS object.
