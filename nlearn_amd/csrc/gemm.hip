@@ -23,6 +23,9 @@
 //     operand then arrives in 128-byte pieces of each row: when the previous
 //     kernel has just written it, it comes from DRAM, where 64-byte pieces
 //     (32-k stages) ran a third slower.
+//   * 256 x 256 tiles (8 waves, the LM head) bound by the CU's global -> LDS
+//     path; in the weight-gradient (TN) form half of the waves issue each
+//     stage's DMA, so one wave per SIMD computes while the other queues loads.
 //   * Workgroup ids are remapped so each XCD (own L2) walks a contiguous run of
 //     tiles in groups of 8 M-tiles, sharing A and B panels in its L2.
 //   * Small outputs with a long reduction (weight gradients) split K across
