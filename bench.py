@@ -335,7 +335,17 @@ def busy_summary(trace_dir: str, steps: int, bs: int, seq: int) -> None:
     for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
             rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
-    rows.sort()
+    out = busy_stats(rows, steps, bs, seq)
+    path = os.path.join(os.path.dirname(TRAFFIC_FILE), f"busy_bs{bs}_seq{seq}.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps({k: out[k] for k in ("wall_ms_per_step", "busy_union_ms_per_step", "busy_ratio",
+                                          "kernel_sum_over_wall")}))
+
+
+def busy_stats(rows, steps: int, bs: int, seq: int) -> dict:
+    """The busy_summary figures from (start_ns, end_ns, kernel_name) rows."""
+    rows = sorted(rows)
     starts = [t0 for t0, _, name in rows if BUSY_FIRST_KERNEL in name]
     if len(starts) < steps + 1:
         raise SystemExit(f"busy-summary: found {len(starts)} step starts, need {steps + 1}")
@@ -370,11 +380,7 @@ def busy_summary(trace_dir: str, steps: int, bs: int, seq: int) -> None:
            "kernel_sum_over_wall": round(total / wall, 4),
            "kernels_ms_per_step": {k: {"ms": round(v[0] / steps / 1e6, 4), "calls": round(v[1] / steps, 2)}
                                    for k, v in sorted(per.items(), key=lambda kv: -kv[1][0])}}
-    path = os.path.join(os.path.dirname(TRAFFIC_FILE), f"busy_bs{bs}_seq{seq}.json")
-    with open(path, "w") as f:
-        json.dump(out, f, indent=1)
-    print(json.dumps({k: out[k] for k in ("wall_ms_per_step", "busy_union_ms_per_step", "busy_ratio",
-                                          "kernel_sum_over_wall")}))
+    return out
 
 
 def flash_probe(n: int, S: int, reps: int = 5) -> None:

@@ -32,3 +32,52 @@ def test_padded_empty_row_strides():
     for (r, c), ld in cases.items():
         t = padded_empty(r, c, torch.bfloat16, "cpu")
         assert t.shape == (r, c) and t.stride() == (ld, 1), (c, t.stride())
+
+
+def _bench_module():
+    import importlib.util
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "bench.py")
+    spec = importlib.util.spec_from_file_location("nlearn_bench", path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod, path
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """The bench measures one GPU: --gpus above 1 exits with status 2 and says so."""
+    import subprocess
+    import sys
+
+    _, path = _bench_module()
+    r = subprocess.run([sys.executable, path, "--gpus", "2"], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+
+
+def test_busy_stats_counts_overlap_once():
+    """The busy ratio is the union of kernel intervals over the replay window
+    (from the first of the last `steps` step starts, marked by the embedding
+    kernel, to the last kernel's end). Per step here: the embedding [0, 100),
+    A [100, 500) and B [300, 700) overlapping by 200, C [800, 900): union 800
+    of a 1000 ns step, kernel sum 1000. A warm-up step before the window is
+    left out."""
+    bench, _ = _bench_module()
+    rows = []
+    for t in (0, 1000, 2000, 3000):
+        rows += [(t, t + 100, "void nl::(anonymous namespace)::embed_fwd_kernel(int, int)"),
+                 (t + 100, t + 500, "void nl::(anonymous namespace)::gemm2_kernel<128, 128>(nl::GemmArgs)"),
+                 (t + 300, t + 700, "void nl::(anonymous namespace)::ln_bwd_kernel<1>(int)"),
+                 (t + 800, t + 900, "void nl::(anonymous namespace)::mean_kernel(float const*, int, float*)")]
+    out = bench.busy_stats(rows, steps=3, bs=2, seq=8)
+    wall = 3900 - 1000
+    assert out["replays"] == 3
+    assert out["busy_ratio"] == round(3 * 800 / wall, 4)
+    assert out["kernel_sum_over_wall"] == round(3 * 1000 / wall, 4)
+    assert out["wall_ms_per_step"] == round(wall / 3 / 1e6, 4)
+    k = out["kernels_ms_per_step"]
+    assert set(k) == {"embed_fwd_kernel", "gemm2_kernel<128, 128>", "ln_bwd_kernel<1>", "mean_kernel"}
+    assert k["gemm2_kernel<128, 128>"] == {"ms": round(400 / 1e6, 4), "calls": 1.0}
+    with pytest.raises(SystemExit):
+        bench.busy_stats(rows, steps=4, bs=2, seq=8)   # needs one step start more than the window holds
