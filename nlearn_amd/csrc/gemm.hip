@@ -185,7 +185,7 @@ __device__ __forceinline__ void epilogue_apply(const GemmArgs& g, int64_t m, int
 }
 
 // Epilogue with its operands fetched from global memory, dispatching on g.epi
-// (the split-K reduction and the register-staged kernel).
+// (the split-K reduction).
 template <typename OutT>
 __device__ __forceinline__ void epilogue4_any(const GemmArgs& g, int64_t m, int n, float v[4]) {
   const bool full = n + 4 <= g.N;
