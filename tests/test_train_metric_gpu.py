@@ -5,7 +5,7 @@
   weight-gradient stream and the deferred LayerNorm sums on (as in the bench),
   then two more steps through the captured HIP graph; through both loss paths
   (LM head + CE, and linear_cross_entropy). Constant lr 1e-3 (the peak lr).
-* configs[0] with BASELINE.md's parity companion: bs4 x seq512, AdamW lr 3e-4,
+* configs[0] with the baseline's parity companion run: bs4 x seq512, AdamW lr 3e-4,
   a 20-step loss curve through the HIP graph from the same initial weights
   and batches as the oracle.
 
