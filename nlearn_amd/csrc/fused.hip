@@ -55,6 +55,11 @@ __device__ __forceinline__ void load8f(const float* p, float f[8]) {
 
 // y = LN(s), s = x (+ r). With r, s is rounded to bf16 and stored to s_out (the
 // residual stream the next block reads) before it is normalised.
+// Rows per wave: short rows (D <= 1024) are handled several per wave, every
+// row's loads issued before the first is used, gamma and beta loaded once.
+template <int VPL>
+constexpr int ln_fwd_rows_per_wave() { return VPL == 1 ? 4 : VPL == 2 ? 2 : 1; }
+
 template <int VPL>
 __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, int D, const uint16_t* __restrict__ x,
                                                                     const uint16_t* __restrict__ r,
@@ -63,14 +68,21 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, in
                                                                     const float* __restrict__ beta,
                                                                     uint16_t* __restrict__ y, float* __restrict__ mean_out,
                                                                     float* __restrict__ rstd_out, float eps) {
+  constexpr int RPW = ln_fwd_rows_per_wave<VPL>();
   const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int64_t off = (int64_t)row * D;
-  // every load of the row (x, r, gamma, beta) is issued before the first use
-  u32x4 xv[VPL], rv[VPL];
-  load_row<VPL>(xv, x + off, D, lane);
-  if (r) load_row<VPL>(rv, r + off, D, lane);
+  const int wave = threadIdx.x >> 6;
+  const int row0 = blockIdx.x * kRowsPerBlock * RPW + wave;  // rows row0 + k * kRowsPerBlock
+  if (row0 >= rows) return;
+  // every load of the wave's rows (x, r) and of gamma, beta is issued before the first use
+  u32x4 xv[RPW][VPL], rv[RPW][VPL];
+#pragma unroll
+  for (int k = 0; k < RPW; ++k) {
+    const int row = row0 + k * kRowsPerBlock;
+    if (row < rows) {
+      load_row<VPL>(xv[k], x + (int64_t)row * D, D, lane);
+      if (r) load_row<VPL>(rv[k], r + (int64_t)row * D, D, lane);
+    }
+  }
   float gg[VPL][8], bb[VPL][8];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) {
@@ -80,50 +92,56 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void ln_fwd_kernel(int rows, in
       load8f(beta + c, bb[i]);
     }
   }
-  float f[VPL][8];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) unpack8(xv[i], f[i]);
-  if (r) {
+  for (int k = 0; k < RPW; ++k) {
+    const int row = row0 + k * kRowsPerBlock;
+    if (row >= rows) break;
+    const int64_t off = (int64_t)row * D;
+    float f[VPL][8];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) unpack8(xv[k][i], f[i]);
+    if (r) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float g[8];
+        unpack8(rv[k][i], g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[i][j] = bf16_to_f32(f32_to_bf16(f[i][j] + g[j]));
+        const int c = (i * 64 + lane) * 8;
+        if (c < D) *reinterpret_cast<u32x4*>(s_out + off + c) = pack8(f[i]);
+      }
+    }
+    // columns beyond D hold zeros, so they add nothing to the sum
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += f[i][j];
+    const float mean = wave_sum(s) / (float)D;
+    float v = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      float g[8];
-      unpack8(rv[i], g);
+      const bool in = (i * 64 + lane) * 8 < D;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) f[i][j] = bf16_to_f32(f32_to_bf16(f[i][j] + g[j]));
+      for (int j = 0; j < 8; ++j) {
+        const float d = in ? f[i][j] - mean : 0.f;
+        v += d * d;
+      }
+    }
+    const float rstd = rsqrtf(wave_sum(v) / (float)D + eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
       const int c = (i * 64 + lane) * 8;
-      if (c < D) *reinterpret_cast<u32x4*>(s_out + off + c) = pack8(f[i]);
+      if (c >= D) continue;
+      float o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = (f[i][j] - mean) * rstd * gg[i][j] + bb[i][j];
+      *reinterpret_cast<u32x4*>(y + off + c) = pack8(o);
     }
-  }
-  // columns beyond D hold zeros, so they add nothing to the sum
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) s += f[i][j];
-  const float mean = wave_sum(s) / (float)D;
-  float v = 0.f;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const bool in = (i * 64 + lane) * 8 < D;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float d = in ? f[i][j] - mean : 0.f;
-      v += d * d;
+    if (lane == 0) {
+      mean_out[row] = mean;
+      rstd_out[row] = rstd;
     }
-  }
-  const float rstd = rsqrtf(wave_sum(v) / (float)D + eps);
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    const int c = (i * 64 + lane) * 8;
-    if (c >= D) continue;
-    float o[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = (f[i][j] - mean) * rstd * gg[i][j] + bb[i][j];
-    *reinterpret_cast<u32x4*>(y + off + c) = pack8(o);
-  }
-  if (lane == 0) {
-    mean_out[row] = mean;
-    rstd_out[row] = rstd;
   }
 }
 
@@ -532,14 +550,16 @@ extern "C" int nl_layernorm_fwd(void* stream, int rows, int D, const nl_bf16* x,
   if ((((uintptr_t)x | (uintptr_t)y | (uintptr_t)gamma | (uintptr_t)beta | (uintptr_t)residual | (uintptr_t)sum_out) &
        15) != 0)
     return nl_set_error(NL_EALIGN, "layernorm: buffers must be 16-byte aligned");
-  dim3 grid((rows + kRowsPerBlock - 1) / kRowsPerBlock), block(64 * kRowsPerBlock);
+  const dim3 block(64 * kRowsPerBlock);
   hipStream_t st = (hipStream_t)stream;
   switch (vectors_per_lane(D)) {
 #define NL_LNF(N)                                                                                                    \
-  case N:                                                                                                            \
-    hipLaunchKernelGGL(ln_fwd_kernel<N>, grid, block, 0, st, rows, D, x, residual, sum_out, gamma, beta, y, mean, rstd, \
-                       eps);                                                                                         \
-    break;
+  case N: {                                                                                                          \
+    const int per = kRowsPerBlock * ln_fwd_rows_per_wave<N>();                                                       \
+    hipLaunchKernelGGL(ln_fwd_kernel<N>, dim3((rows + per - 1) / per), block, 0, st, rows, D, x, residual, sum_out,  \
+                       gamma, beta, y, mean, rstd, eps);                                                             \
+    break;                                                                                                           \
+  }
     NL_LNF(1)
     NL_LNF(2)
     NL_LNF(4)
