@@ -130,3 +130,19 @@ def test_jax_ffi_binding_registers_only_defined_handlers():
             "ce_bwd"} <= targets
     called = set(re.findall(r"\b(nl_[a-z0-9_]+)\s*\(", code)) - defined
     assert called and called <= set(header_functions()), called - set(header_functions())
+
+
+def test_ctypes_table_matches_header_arity():
+    """Every ctypes signature in nlearn_amd._lib has as many arguments as the
+    header's declaration of that entry point (a missing or extra argument
+    would shift every later one)."""
+    from nlearn_amd import _lib
+
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    decls = dict((m.group(1), m.group(2)) for m in re.finditer(r"\b(nl_[a-z0-9_]+)\s*\(([^()]*)\)\s*;", text))
+    assert set(decls) == set(_lib.EXPORTED)
+    for name, params in decls.items():
+        params = " ".join(params.split())
+        n = 0 if params in ("", "void") else params.count(",") + 1
+        assert n == len(_lib._SIGNATURES[name]), (name, n, len(_lib._SIGNATURES[name]))
