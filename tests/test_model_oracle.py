@@ -80,6 +80,93 @@ def test_adamw_closed_form_first_steps():
     assert p["w"][0] == pytest.approx(1.0 - 0.1 * (2.0 / (2.0 + 1e-8) + 0.5 * 1.0), rel=1e-12)
 
 
+def test_adamw_constant_gradient_closed_form_every_step():
+    """With a constant gradient g, m_t = (1 - b1^t) g and v_t = (1 - b2^t) g^2,
+    so the bias-corrected moments are g and g^2 at EVERY t and each update is
+    lr_t * (g / (|g| + eps) + wd * p). A bias correction frozen at t = 1 (or a
+    count that does not advance) moves the t >= 2 updates off this."""
+    lrs = [0.1, 0.05, 0.02, 0.3, 0.01]
+    p = {"a": np.array([1.0, -2.0], np.float64), "b": np.array([[0.5]], np.float64)}
+    g = {"a": np.array([3.0, -0.25]), "b": np.array([[1e-3]])}
+    opt = om.AdamWNP(p, lambda c: lrs[c], wd=0.2)
+    want = {k: v.copy() for k, v in p.items()}
+    for t in range(len(lrs)):
+        opt.step(p, g)
+        for k in want:
+            want[k] = want[k] - lrs[t] * (g[k] / (np.abs(g[k]) + 1e-8) + 0.2 * want[k])
+            np.testing.assert_allclose(p[k], want[k], rtol=1e-12, atol=1e-15, err_msg=f"update {t + 1}, leaf {k}")
+
+
+def test_adamw_second_and_third_updates_by_hand():
+    """Changing gradients: the moments and bias corrections written out by
+    hand for t = 2 and t = 3 (optax.adamw, train.py:504-505)."""
+    b1, b2, eps, wd = 0.9, 0.999, 1e-8, 0.1
+    g1, g2, g3 = 2.0, -0.5, 0.75
+    lr = {0: 0.1, 1: 0.04, 2: 0.07}
+    p = {"w": np.array([1.5], np.float64)}
+    opt = om.AdamWNP(p, lambda c: lr[c], wd=wd)
+    w = 1.5
+    # t = 1
+    opt.step(p, {"w": np.array([g1])})
+    w = w - lr[0] * (g1 / (abs(g1) + eps) + wd * w)
+    assert p["w"][0] == pytest.approx(w, rel=1e-13)
+    # t = 2: m = b1 (1-b1) g1 + (1-b1) g2, v = b2 (1-b2) g1^2 + (1-b2) g2^2
+    opt.step(p, {"w": np.array([g2])})
+    m2 = b1 * (1 - b1) * g1 + (1 - b1) * g2
+    v2 = b2 * (1 - b2) * g1 ** 2 + (1 - b2) * g2 ** 2
+    w = w - lr[1] * ((m2 / (1 - b1 ** 2)) / (math.sqrt(v2 / (1 - b2 ** 2)) + eps) + wd * w)
+    assert p["w"][0] == pytest.approx(w, rel=1e-13)
+    # t = 3
+    opt.step(p, {"w": np.array([g3])})
+    m3 = b1 ** 2 * (1 - b1) * g1 + b1 * (1 - b1) * g2 + (1 - b1) * g3
+    v3 = b2 ** 2 * (1 - b2) * g1 ** 2 + b2 * (1 - b2) * g2 ** 2 + (1 - b2) * g3 ** 2
+    w = w - lr[2] * ((m3 / (1 - b1 ** 3)) / (math.sqrt(v3 / (1 - b2 ** 3)) + eps) + wd * w)
+    assert p["w"][0] == pytest.approx(w, rel=1e-13)
+    assert opt.count == 3
+
+
+def test_adamw_clipped_second_update_by_hand():
+    """optax.chain(clip_by_global_norm(1), adamw): update 1 below the threshold
+    passes g untouched; update 2's global norm over both leaves is 5, so the
+    gradient enters the moments as g * 1/5 (train.py:502-506)."""
+    b1, b2, eps, wd = 0.9, 0.999, 1e-8, 0.1
+    p = {"a": np.array([1.0], np.float64), "b": np.array([2.0], np.float64)}
+    opt = om.AdamWNP(p, lambda c: 0.05, wd=wd, clip_norm=1.0)
+    ga1, gb1 = 0.3, -0.4            # norm 0.5 < 1: unclipped
+    ga2, gb2 = 3.0, 4.0             # norm 5 >= 1: scaled to (0.6, 0.8)
+    opt.step(p, {"a": np.array([ga1]), "b": np.array([gb1])})
+    opt.step(p, {"a": np.array([ga2]), "b": np.array([gb2])})
+    for w0, g1, g2, k in ((1.0, ga1, ga2 / 5, "a"), (2.0, gb1, gb2 / 5, "b")):
+        w = w0 - 0.05 * (g1 / (abs(g1) + eps) + wd * w0)
+        m2 = b1 * (1 - b1) * g1 + (1 - b1) * g2
+        v2 = b2 * (1 - b2) * g1 ** 2 + (1 - b2) * g2 ** 2
+        w = w - 0.05 * ((m2 / (1 - b1 ** 2)) / (math.sqrt(v2 / (1 - b2 ** 2)) + eps) + wd * w)
+        assert p[k][0] == pytest.approx(w, rel=1e-12), k
+
+
+def test_multisteps_k2_by_hand():
+    """optax.MultiSteps(adamw, 2): parameters unchanged on odd calls; the even
+    call applies AdamW to the mean of the two micro-gradients, and the
+    schedule count advances once per update (train.py:319-325,507-508)."""
+    b1, b2, eps, wd = 0.9, 0.999, 1e-8, 0.1
+    lr = {0: 0.1, 1: 0.02}
+    p = {"w": np.array([1.0], np.float64)}
+    ms = om.MultiStepsNP(om.AdamWNP(p, lambda c: lr[c], wd=wd), 2)
+    ms.step(p, {"w": np.array([1.0])})
+    assert p["w"][0] == 1.0
+    ms.step(p, {"w": np.array([3.0])})          # mean 2
+    w = 1.0 - lr[0] * (2.0 / (2.0 + eps) + wd * 1.0)
+    assert p["w"][0] == pytest.approx(w, rel=1e-13)
+    ms.step(p, {"w": np.array([-1.0])})
+    assert p["w"][0] == pytest.approx(w, rel=1e-13)
+    ms.step(p, {"w": np.array([0.0])})          # mean -0.5
+    m2 = b1 * (1 - b1) * 2.0 + (1 - b1) * -0.5
+    v2 = b2 * (1 - b2) * 4.0 + (1 - b2) * 0.25
+    w = w - lr[1] * ((m2 / (1 - b1 ** 2)) / (math.sqrt(v2 / (1 - b2 ** 2)) + eps) + wd * w)
+    assert p["w"][0] == pytest.approx(w, rel=1e-13)
+    assert ms.inner.count == 2
+
+
 def test_warmup_cosine_schedule_known_points():
     f = lambda c: om.warmup_cosine(c, 1e-3, 200, 1000, 1e-4)
     assert f(0) == 0.0
