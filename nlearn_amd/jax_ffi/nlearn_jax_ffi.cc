@@ -24,9 +24,13 @@
 // 1/sqrt(d) for flash, 1/M for the CE gradient.
 //
 // Boundary dtype: bf16 tensors where the reference passes f32 after its
-// astype(jnp.float32) casts (attention.py:96-99,115; cross_entropy.py:76);
-// those casts become astype(jnp.bfloat16). L, D, loss, lse and the GEMM's C
-// stay f32.
+// astype(jnp.float32) casts (attention.py:97,104,115; cross_entropy.py:76);
+// those casts become astype(jnp.bfloat16), and the results declared for O,
+// dQ, dK, dV and dlogits (attention.py:88,119,124-125; cross_entropy.py:44)
+// become jnp.bfloat16 with them. L, D (attention.py:116, reduced from f32
+// upcasts of dO and O), loss, lse and the GEMM's C stay f32.
+// register.py's CALL_SITES lists every operand and result dtype with its
+// reference line; the bindings at the end of this file must equal it.
 //
 // Alignment: the kernels need 16-byte row starts for the GEMM (ld % 8 == 0).
 // The gemm handlers take dense XLA buffers, so K and N must be multiples of 8:

@@ -132,6 +132,82 @@ def test_jax_ffi_binding_registers_only_defined_handlers():
     assert called and called <= set(header_functions()), called - set(header_functions())
 
 
+def _ffi_handlers():
+    """{handler symbol: (arg dtypes, result dtypes)} from the binding macros
+    of nlearn_jax_ffi.cc, after checking that each handler function's C++
+    parameter list has the same Buffer / ResultBuffer dtypes in the same order
+    (the file is not compiled here, so nothing else would notice)."""
+    src = (ROOT / "nlearn_amd" / "jax_ffi" / "nlearn_jax_ffi.cc").read_text()
+    code = re.sub(r"//[^\n]*", "", src)
+    out = {}
+    for m in re.finditer(r"XLA_FFI_DEFINE_HANDLER_SYMBOL\(\s*(\w+)\s*,\s*(\w+)\s*,(.*?)\);", code, flags=re.S):
+        sym, fn, binding = m.group(1), m.group(2), m.group(3)
+        seq = re.findall(r"NL_(ARG|RET)\((\w+)\)", binding)
+        args = tuple(t for k, t in seq if k == "ARG")
+        rets = tuple(t for k, t in seq if k == "RET")
+        assert [k for k, _ in seq] == ["ARG"] * len(args) + ["RET"] * len(rets), sym
+        sig = re.search(r"ffi::Error\s+" + fn + r"\s*\((.*?)\)\s*\{", code, flags=re.S)
+        assert sig, fn
+        params = re.findall(r"ffi::(Buffer|ResultBuffer)<ffi::(\w+)>", sig.group(1))
+        assert tuple(t for k, t in params if k == "Buffer") == args, (fn, params, args)
+        assert tuple(t for k, t in params if k == "ResultBuffer") == rets, (fn, params, rets)
+        out[sym] = (args, rets)
+    return out
+
+
+def test_jax_ffi_handler_dtypes_match_the_edited_reference_call_sites():
+    """Every handler binds exactly the operand and result dtypes that the
+    reference's ffi_call sites pass once edited as documented (bf16 tensors,
+    f32 L / D / loss / lse / GEMM C): a mismatch is rejected by XLA when it
+    decodes the call. Where /root/reference exists, every cited line is
+    checked against it: each result line is a jax.ShapeDtypeStruct declared
+    float32 today, the list of edited ones covers every ShapeDtypeStruct in
+    the three wrappers that a bf16 handler result replaces, and every operand
+    line is an astype / the D reduction."""
+    from nlearn_amd.jax_ffi import register
+
+    handlers = _ffi_handlers()
+    for target, sym in register.TARGETS:
+        args, rets = register.CALL_SITES[target]
+        assert handlers[sym] == (tuple(a for a, _ in args), tuple(r for r, _ in rets)), target
+        for dt, line in rets:
+            assert (dt == "BF16") == (line in register.EDITED_RESULTS) or line.startswith("gemm.py"), (target, line)
+    assert set(register.CALL_SITES) == {t for t, _ in register.TARGETS}
+
+    ref = Path("/root/reference/nlearn")
+    if not ref.is_dir():
+        pytest.skip("reference sources absent: the cited lines were checked where they exist")
+    files = {"attention.py": ref / "attention.py", "gemm.py": ref / "kernels" / "gemm.py",
+             "cross_entropy.py": ref / "kernels" / "cross_entropy.py"}
+    lines = {k: v.read_text().splitlines() for k, v in files.items()}
+
+    def at(cite):
+        f, n = cite.split(":")
+        return lines[f][int(n) - 1]
+
+    cited_results = set()
+    for target, (args, rets) in register.CALL_SITES.items():
+        for dt, cite in rets:
+            if target in ("ce_fwd_bwd", "gemm_nt", "gemm_tn"):
+                continue  # new targets reuse the results of the ones they replace
+            assert "jax.ShapeDtypeStruct(" in at(cite) and "jnp.float32" in at(cite), (target, cite, at(cite))
+            cited_results.add(cite)
+        for dt, cite in args:
+            text = at(cite)
+            if dt == "F32" and cite == "attention.py:116":
+                assert text.lstrip().startswith("D = jnp.sum("), text
+            elif cite == "attention.py:89":
+                assert "jax.ShapeDtypeStruct((n, s)" in text, text
+            elif cite.startswith("cross_entropy.py:3"):
+                assert "jax.ShapeDtypeStruct((M,)" in text, text
+            else:
+                assert ".astype(" in text, (cite, text)
+    # every result declaration of the six reference targets is accounted for
+    declared = {f"{f}:{i + 1}" for f, ls in lines.items() for i, t in enumerate(ls) if "jax.ShapeDtypeStruct(" in t}
+    assert declared == cited_results, declared ^ cited_results
+    assert register.EDITED_RESULTS <= declared
+
+
 def test_ctypes_table_matches_header_arity():
     """Every ctypes signature in nlearn_amd._lib has as many arguments as the
     header's declaration of that entry point (a missing or extra argument
