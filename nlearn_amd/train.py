@@ -27,6 +27,9 @@ import argparse
 import contextlib
 import math
 import os
+import signal
+import sys
+import threading
 import time
 
 import torch
@@ -388,6 +391,7 @@ def make_train_step(optimizer, cfg: ModelConfig = BASELINE, graph: bool = False,
 
     fused_lmhead: the loss through linear_cross_entropy (see ``batch_loss``).
     """
+    check_hw_queues()
     overlap = wgrad.overlap_weight_grads if overlap_wgrad else _no_overlap
     scale = LOSS_SCALE if loss_scale is None else float(loss_scale)
     if not scale > 0:
@@ -415,6 +419,32 @@ def make_train_step(optimizer, cfg: ModelConfig = BASELINE, graph: bool = False,
 @contextlib.contextmanager
 def _no_overlap(device=None):
     yield
+
+
+# The fewest hardware queues per device the training step has run with. The
+# HIP runtime maps streams onto GPU_MAX_HW_QUEUES queues (default 4); the step
+# uses up to three streams of its own (the current one, the weight-gradient
+# stream, the op-internal side stream) plus graph capture's. It has run with
+# 4, 8 and 16 queues. A process with GPU_MAX_HW_QUEUES=2 ended in a host
+# segmentation fault before its first timed step, with no error from any HIP
+# call; the cause was not found, so fewer queues than 4 are refused.
+MIN_HW_QUEUES = 4
+
+
+def check_hw_queues(env=None) -> None:
+    """Raise if GPU_MAX_HW_QUEUES asks for fewer hardware queues than the step
+    has been run with (see MIN_HW_QUEUES); unset or unparsable values leave the
+    runtime's default of 4."""
+    raw = (os.environ if env is None else env).get("GPU_MAX_HW_QUEUES")
+    try:
+        n = int(raw) if raw is not None else None
+    except ValueError:
+        n = None
+    if n is not None and 0 < n < MIN_HW_QUEUES:
+        raise RuntimeError(
+            f"GPU_MAX_HW_QUEUES={n}: the training step has only been run with {MIN_HW_QUEUES} or more hardware "
+            f"queues per device (a run with 2 ended in a segmentation fault whose cause is not known); "
+            f"unset it or set it to at least {MIN_HW_QUEUES}")
 
 
 class _GraphedStep:
@@ -484,15 +514,48 @@ class SyntheticTokens:
                              dtype=torch.int32)
 
 
+class GracefulStop:
+    """SIGINT / SIGTERM set a flag instead of ending the process; the loop
+    checks it after each step (train.py:556-562). Installed only from the main
+    thread (Python delivers signals there); the previous handlers come back on
+    exit."""
+
+    SIGNALS = (signal.SIGINT, signal.SIGTERM)
+
+    def __init__(self):
+        self.requested = False
+        self._old = {}
+
+    def _handle(self, signum, frame):
+        print("\nInterrupt received — will save checkpoint and exit after this step.", flush=True)
+        self.requested = True
+
+    def __enter__(self):
+        if threading.current_thread() is threading.main_thread():
+            for sig in self.SIGNALS:
+                self._old[sig] = signal.signal(sig, self._handle)
+        return self
+
+    def __exit__(self, *exc):
+        for sig, old in self._old.items():
+            signal.signal(sig, old)
+        self._old.clear()
+        return False
+
+
 def train(steps: int = 20, seq_len: int = 512, seed: int = 0, batch_size: int = BATCH_SIZE,
           peak_lr: float = PEAK_LR, log_every: int = 10, cfg: ModelConfig | None = None, run_name=None,
           resume: bool = False, checkpoint_every: int = CHECKPOINT_EVERY) -> list:
     """Offline training loop; returns the per-step losses of the steps it ran.
 
-    As the reference's loop (train.py:537-605): every ``checkpoint_every``
+    As the reference's loop (train.py:537-622): every ``checkpoint_every``
     steps it saves the parameters and the full resume state; ``resume=True``
     continues from ``resume.pkl`` of ``run_name`` when one exists (parameters,
-    optimizer state incl. the schedule position, next step)."""
+    optimizer state incl. the schedule position, next step). SIGINT or SIGTERM
+    finishes the current step, saves the parameters (``step_NNNNNN.pkl`` of
+    that step) and the resume state, and exits the process with status 0
+    (train.py:556-562,604-609). The last step's parameters are saved as
+    ``step_<steps>.pkl`` (train.py:612)."""
     cfg = cfg or ModelConfig(max_seq_len=max(seq_len, BASELINE.max_seq_len))
     # with GRAD_ACCUM micro-steps per update the schedule advances per
     # effective update (train.py:483-495)
@@ -517,16 +580,25 @@ def train(steps: int = 20, seq_len: int = 512, seed: int = 0, batch_size: int = 
     data = SyntheticTokens(batch_size, seq_len, cfg.vocab_size, seed + start)
     losses = []
     t0 = time.time()
-    for step in range(start, steps):
-        params, state, loss = step_fn(params, state, data.get_batch())
-        losses.append(loss)
-        if (step + 1) % log_every == 0 or step + 1 == steps:
-            torch.cuda.synchronize()
-            dt = time.time() - t0
-            print(f"step {step + 1:5d}  loss {loss.item():.4f}  {(step + 1 - start) * batch_size * seq_len / dt:,.0f} tok/s")
-        if step > 0 and checkpoint_every > 0 and step % checkpoint_every == 0:
-            save_checkpoint(params, step, run_name=run_name)
-            save_resume_state(params, state, step + 1, run_name=run_name)
+    with GracefulStop() as stop:
+        for step in range(start, steps):
+            params, state, loss = step_fn(params, state, data.get_batch())
+            losses.append(loss)
+            if (step + 1) % log_every == 0 or step + 1 == steps:
+                torch.cuda.synchronize()
+                dt = time.time() - t0
+                print(f"step {step + 1:5d}  loss {loss.item():.4f}  "
+                      f"{(step + 1 - start) * batch_size * seq_len / dt:,.0f} tok/s", flush=True)
+            if step > 0 and checkpoint_every > 0 and step % checkpoint_every == 0:
+                save_checkpoint(params, step, run_name=run_name)
+                save_resume_state(params, state, step + 1, run_name=run_name)
+            if stop.requested:
+                print("Saving checkpoint before exit...", flush=True)
+                save_checkpoint(params, step, run_name=run_name)
+                save_resume_state(params, state, step + 1, run_name=run_name)
+                sys.exit(0)
+    if steps > start:
+        save_checkpoint(params, steps, run_name=run_name)
     return [float(l) for l in torch.stack(losses).cpu()] if losses else []
 
 

@@ -81,3 +81,39 @@ def test_busy_stats_counts_overlap_once():
     assert k["gemm2_kernel<128, 128>"] == {"ms": round(400 / 1e6, 4), "calls": 1.0}
     with pytest.raises(SystemExit):
         bench.busy_stats(rows, steps=4, bs=2, seq=8)   # needs one step start more than the window holds
+
+
+def test_train_step_refuses_fewer_hardware_queues_than_tested(monkeypatch):
+    """GPU_MAX_HW_QUEUES below 4 (a 2-queue process once ended in a host
+    segmentation fault of unknown cause) is refused when the step is built,
+    before anything touches the GPU; 4 and more, unset or unparsable pass."""
+    from nlearn_amd import train as tr
+
+    for bad in ("1", "2", "3"):
+        with pytest.raises(RuntimeError, match="GPU_MAX_HW_QUEUES"):
+            tr.check_hw_queues({"GPU_MAX_HW_QUEUES": bad})
+    for ok in ({}, {"GPU_MAX_HW_QUEUES": "4"}, {"GPU_MAX_HW_QUEUES": "16"}, {"GPU_MAX_HW_QUEUES": "x"}):
+        tr.check_hw_queues(ok)
+    monkeypatch.setenv("GPU_MAX_HW_QUEUES", "2")
+    with pytest.raises(RuntimeError, match="at least 4"):
+        tr.make_train_step(tr.AdamW(1e-3))
+    monkeypatch.setenv("GPU_MAX_HW_QUEUES", "4")
+    assert callable(tr.make_train_step(tr.AdamW(1e-3)))
+
+
+def test_graceful_stop_turns_sigterm_and_sigint_into_a_flag():
+    """train()'s interrupt handling (train.py:556-562): inside GracefulStop a
+    SIGTERM or SIGINT only sets the flag the loop checks after each step; the
+    previous handlers are back afterwards."""
+    import os
+    import signal
+
+    from nlearn_amd.train import GracefulStop
+
+    before = {s: signal.getsignal(s) for s in (signal.SIGINT, signal.SIGTERM)}
+    for sig in (signal.SIGTERM, signal.SIGINT):
+        with GracefulStop() as stop:
+            assert not stop.requested
+            os.kill(os.getpid(), sig)   # the Python-level handler runs before the next bytecode
+            assert stop.requested
+        assert {s: signal.getsignal(s) for s in before} == before

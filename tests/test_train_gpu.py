@@ -170,3 +170,58 @@ def test_full_gradient_finite_at_seq_8192_both_loss_paths(dev):
     assert abs(out[0][0] - out[1][0]) < 1e-3
     for i, (a, b) in enumerate(zip(out[0][1], out[1][1])):
         assert rel_l2(b, a, floor=1e-8) < 1e-2, i
+
+
+def test_sigterm_saves_checkpoint_and_resume_state_then_exits_zero(dev, tmp_path):
+    """train()'s interrupt path (train.py:556-562,604-609): SIGTERM sent to a
+    process running train() lets the current step finish, saves that step's
+    parameters and the resume state, and ends the process with status 0; the
+    resume state then names the next step and loads."""
+    import queue
+    import signal
+    import subprocess
+    import sys
+    import threading
+
+    from nlearn_amd.checkpoint import load_checkpoint
+    from nlearn_amd.model import tree_leaves
+    from nlearn_amd.train import AdamW, load_resume_state
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = ("from nlearn_amd.model import ModelConfig\n"
+            "from nlearn_amd.train import train\n"
+            "train(steps=100000, seq_len=64, batch_size=2, log_every=1, cfg=ModelConfig(max_seq_len=64), "
+            "run_name='sig', checkpoint_every=0)\n")
+    env = dict(os.environ, PYTHONPATH=root + os.pathsep + os.environ.get("PYTHONPATH", ""))
+    proc = subprocess.Popen([sys.executable, "-u", "-c", code], cwd=tmp_path, env=env, stdout=subprocess.PIPE,
+                            stderr=subprocess.STDOUT, text=True)
+    lines: queue.Queue = queue.Queue()
+    threading.Thread(target=lambda: [lines.put(l) for l in proc.stdout], daemon=True).start()
+    out = []
+    try:
+        while not any(l.startswith("step     3") for l in out):
+            out.append(lines.get(timeout=120))
+        proc.send_signal(signal.SIGTERM)
+        rc = proc.wait(timeout=120)
+    finally:
+        if proc.poll() is None:
+            proc.kill()
+            proc.wait()
+    while not lines.empty():
+        out.append(lines.get())
+    text = "".join(out)
+    assert rc == 0, text[-2000:]
+    assert "Interrupt received" in text and "Saving checkpoint before exit" in text, text[-2000:]
+    last = max(int(l.split()[1]) for l in out if l.startswith("step "))     # steps printed 1-based
+    ck = tmp_path / "checkpoints" / "sig" / f"step_{last - 1:06d}.pkl"
+    assert ck.exists(), sorted(os.listdir(tmp_path / "checkpoints" / "sig"))
+    params_np = load_checkpoint(str(ck))
+    cwd = os.getcwd()
+    os.chdir(tmp_path)
+    try:
+        params, state, nxt = load_resume_state(AdamW(1e-3), run_name="sig", device=dev)
+    finally:
+        os.chdir(cwd)
+    assert nxt == last and state["count"] == last
+    for a, b in zip(tree_leaves(params), tree_leaves(params_np)):
+        assert np.array_equal(a.detach().float().cpu().numpy(), b)
