@@ -34,6 +34,8 @@ def _args():
     ap.add_argument("--batch-size", type=int, default=32)
     ap.add_argument("--seq-len", type=int, default=512)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-variant", action="store_true",
+                    help="skip configs[4]'s bs4 x seq4096 variant (timed after the headline workload)")
     ap.add_argument("--no-graph", action="store_true", help="launch every kernel from Python (no HIP graph)")
     ap.add_argument("--torch-step", action="store_true",
                     help="time the same training step written with plain PyTorch ops (a reference point)")
@@ -685,8 +687,6 @@ def main():
     import torch
 
     from nlearn_amd import _lib
-    from nlearn_amd.model import ModelConfig, flops_per_step, init_model
-    from nlearn_amd.train import AdamW, SyntheticTokens, make_train_step, warmup_cosine_decay_schedule
 
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
@@ -694,91 +694,32 @@ def main():
     _lib.load()
     dev = torch.device("cuda:0")
     bs, seq = a.batch_size, a.seq_len
-    cfg = ModelConfig(max_seq_len=max(512, seq))
-    params = init_model(0, cfg, dev)
-    total_updates = a.warmup + a.steps
-    opt = AdamW(warmup_cosine_decay_schedule(0.0, 1e-3, 200, max(total_updates, 1000), 1e-4))
-    state = opt.init(params)
     graph = not a.no_graph
-    probe = KernelProbe(torch)
-    _lib.set_probe(probe)
-    step = make_train_step(opt, cfg, graph=graph, warmup=2, fused_lmhead=a.fused_lmhead)
-    data = SyntheticTokens(bs, seq, cfg.vocab_size, seed=0, device=dev)
-    batches = [data.get_batch() for _ in range(4)]
-
-    # warm-up (in graph mode the step is captured during it and replayed)
-    for i in range(max(a.warmup, 3 if graph else 0)):
-        params, state, loss = step(params, state, batches[i % 4])
-    torch.cuda.synchronize()
-    torch.cuda.reset_peak_memory_stats()
     if a.replay_probe:
-        for i in range(a.steps):
-            params, state, loss = step(params, state, batches[i % 4])
-        torch.cuda.synchronize()
-        print(json.dumps({"probe": "replay", "steps": a.steps, "loss": round(float(loss), 4)}))
+        run_workload(torch, dev, bs, seq, a.steps, a.warmup, graph, a.fused_lmhead, replay_only=True)
         return
-
-    probe.enabled = not graph
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(a.steps):
-        params, state, loss = step(params, state, batches[i % 4])
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    if graph:
-        # Per-kernel durations: events cannot be placed between the nodes of a
-        # replayed graph (torch-ROCm refuses external events in a capture), so
-        # the same step runs a.steps more times eagerly, every kernel bracketed
-        # by events on its launch stream; kernels, shapes and the two-stream
-        # overlap are those of the replays.
-        eager = make_train_step(opt, cfg, graph=False, fused_lmhead=a.fused_lmhead)
-        probe.enabled = True
-        for i in range(a.steps):
-            params, state, loss = eager(params, state, batches[i % 4])
-        torch.cuda.synchronize()
-    probe.enabled = False
-    # The same step once more on one stream (no weight-gradient overlap): every
-    # kernel alone on the GPU, its own speed without CUs shared with the other
-    # stream.
-    iso_probe = KernelProbe(torch)
-    _lib.set_probe(iso_probe)
-    solo = make_train_step(opt, cfg, graph=False, fused_lmhead=a.fused_lmhead, overlap_wgrad=False)
-    iso_steps = min(a.steps, 5)
-    iso_probe.enabled = True
-    for i in range(iso_steps):
-        params, state, loss = solo(params, state, batches[i % 4])
-    torch.cuda.synchronize()
-    iso_probe.enabled = False
-    _lib.set_probe(None)
-
-    tokens = bs * seq
-    ms = dt / a.steps * 1e3
-    value = tokens * a.steps / dt
-    kernels = probe.summary(a.steps)
-    iso = iso_probe.summary(iso_steps)
-    dom_tag = max(kernels, key=lambda k: kernels[k]["time_per_step_ms"]) if kernels else None
+    r = run_workload(torch, dev, bs, seq, a.steps, a.warmup, graph, a.fused_lmhead)
+    kernels, iso = r["kernels"], r["iso"]
+    dom_tag = dominant_kernel(kernels, iso)
     roof = None
     if dom_tag:
         k = kernels[dom_tag]
         roof = {"bound": k["bound"], "achieved": round(k["achieved"], 2), "peak": k["peak"], "unit": k["unit"],
                 "frac": round(k["frac"], 4), "traffic": load_traffic(dom_tag), "kernel": dom_tag,
                 "avg_us": round(k["avg_us"], 2),
+                "chosen_by": "largest time per step with every kernel alone on the GPU (one-stream pass)",
                 "timing": "in the step: HIP events on the launch stream, two-stream overlap as in the replays",
                 "frac_isolated": round(iso[dom_tag]["frac"], 4) if dom_tag in iso else None,
                 "avg_us_isolated": round(iso[dom_tag]["avg_us"], 2) if dom_tag in iso else None}
-    fl = flops_per_step(cfg, bs, seq)
 
-    def _table(kk):
-        return {k: {kk2: (round(vv, 4) if isinstance(vv, float) else vv) for kk2, vv in v.items()}
-                for k, v in sorted(kk.items(), key=lambda kv: -kv[1]["time_per_step_ms"])}
     out = {
         "metric": "train tokens/sec d512/4L/seq512 bs32 (1 GPU)",
-        "value": round(value, 1),
+        "value": round(r["value"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": a.steps,
         "warmup": a.warmup,
-        "ms_per_step": round(ms, 3),
+        "ms_per_step": round(r["ms"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -791,22 +732,147 @@ def main():
         "roofline": roof,
         "cpu_baseline": None,
         "detail": {
-            "mfu_matmul": round(fl["total"] / (dt / a.steps) / (PEAK_BF16_TFLOPS * 1e12), 4),
-            "matmul_tflop_per_step": round(fl["total"] / 1e12, 4),
-            "six_n_t_tflops": round(fl["six_n_t"] / (dt / a.steps) / 1e12, 2),
-            "peak_hbm_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+            "mfu_matmul": r["mfu"],
+            "matmul_tflop_per_step": r["tflop"],
+            "six_n_t_tflops": r["six_n_t_tflops"],
+            "peak_hbm_gib": r["peak_hbm_gib"],
             "busy": load_busy(bs, seq),
-            "final_loss": round(float(loss.detach()), 4),
+            "final_loss": r["loss"],
             "kernels_in_step": _table(kernels),
             "kernels_isolated": _table(iso),
         },
     }
+    del r
+    # BASELINE configs[4] also asks for the bs4 x seq4096 variant: the same step,
+    # timed the same way in the same process (after the headline's buffers are
+    # freed, so its peak memory is its own)
+    if not a.no_variant and (bs, seq) != VARIANT:
+        vb, vs = VARIANT
+        v = run_workload(torch, dev, vb, vs, min(a.steps, 20), min(a.warmup, 5), graph, a.fused_lmhead)
+        vdom = dominant_kernel(v["kernels"], v["iso"])
+        out["detail"]["variant_bs4_seq4096"] = {
+            "workload": f"train_step fwd+bwd+AdamW d512/8h/4L vocab50257 bs{vb} seq{vs}",
+            "tokens_per_s": round(v["value"], 1), "ms_per_step": round(v["ms"], 3), "steps": v["steps"],
+            "mfu_matmul": v["mfu"], "matmul_tflop_per_step": v["tflop"], "peak_hbm_gib": v["peak_hbm_gib"],
+            "busy": load_busy(vb, vs), "final_loss": v["loss"],
+            "dominant_kernel": None if vdom is None else {
+                "kernel": vdom, "chosen_by": "largest time per step alone on the GPU",
+                "frac": round(v["kernels"][vdom]["frac"], 4), "avg_us": round(v["kernels"][vdom]["avg_us"], 2),
+                "frac_isolated": round(v["iso"][vdom]["frac"], 4),
+                "avg_us_isolated": round(v["iso"][vdom]["avg_us"], 2)},
+            "kernels_isolated": _table(v["iso"]),
+        }
+        del v
     if not a.no_cpu_baseline:
         try:
             out["cpu_baseline"] = cpu_baseline(a.cpu_seconds)
         except ImportError as e:  # oracle absent from the tree
             out["cpu_baseline"] = {"error": str(e)}
     print(json.dumps(out))
+
+
+# BASELINE configs[4]'s second workload
+VARIANT = (4, 4096)
+
+
+def _table(kk):
+    return {k: {kk2: (round(vv, 4) if isinstance(vv, float) else vv) for kk2, vv in v.items()}
+            for k, v in sorted(kk.items(), key=lambda kv: -kv[1]["time_per_step_ms"])}
+
+
+def dominant_kernel(kernels: dict, iso: dict):
+    """The kernel with the largest time per step when every kernel runs alone
+    (the one-stream pass): in the overlapped pass a kernel sharing CUs with the
+    other stream looks longer than it is. Falls back to the overlapped pass."""
+    src = {k: v for k, v in iso.items() if k in kernels} or kernels
+    return max(src, key=lambda k: src[k]["time_per_step_ms"]) if src else None
+
+
+def run_workload(torch, dev, bs: int, seq: int, steps: int, warmup: int, graph: bool, fused: bool,
+                 replay_only: bool = False):
+    """One training workload: warm-up (and capture), ``steps`` timed steps,
+    then the per-kernel passes (overlapped as in the step, and one-stream);
+    returns the figures and frees every buffer it made."""
+    import gc
+
+    from nlearn_amd import _lib
+    from nlearn_amd.model import ModelConfig, flops_per_step, init_model
+    from nlearn_amd.train import AdamW, SyntheticTokens, make_train_step, warmup_cosine_decay_schedule
+
+    gc.collect()
+    torch.cuda.empty_cache()
+    # peak memory of this workload alone: parameters, optimizer state, the
+    # eager warm-up steps, the capture and the timed steps
+    torch.cuda.reset_peak_memory_stats()
+    cfg = ModelConfig(max_seq_len=max(512, seq))
+    params = init_model(0, cfg, dev)
+    total_updates = warmup + steps
+    opt = AdamW(warmup_cosine_decay_schedule(0.0, 1e-3, 200, max(total_updates, 1000), 1e-4))
+    state = opt.init(params)
+    probe = KernelProbe(torch)
+    _lib.set_probe(probe)
+    step = make_train_step(opt, cfg, graph=graph, warmup=2, fused_lmhead=fused)
+    data = SyntheticTokens(bs, seq, cfg.vocab_size, seed=0, device=dev)
+    batches = [data.get_batch() for _ in range(4)]
+
+    # warm-up (in graph mode the step is captured during it and replayed)
+    for i in range(max(warmup, 3 if graph else 0)):
+        params, state, loss = step(params, state, batches[i % 4])
+    torch.cuda.synchronize()
+    if replay_only:
+        for i in range(steps):
+            params, state, loss = step(params, state, batches[i % 4])
+        torch.cuda.synchronize()
+        _lib.set_probe(None)
+        print(json.dumps({"probe": "replay", "steps": steps, "loss": round(float(loss), 4)}))
+        return None
+
+    probe.enabled = not graph
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        params, state, loss = step(params, state, batches[i % 4])
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    peak = torch.cuda.max_memory_allocated()
+    eager = None
+    if graph:
+        # Per-kernel durations: events cannot be placed between the nodes of a
+        # replayed graph (torch-ROCm refuses external events in a capture), so
+        # the same step runs `steps` more times eagerly, every kernel bracketed
+        # by events on its launch stream; kernels, shapes and the two-stream
+        # overlap are those of the replays.
+        eager = make_train_step(opt, cfg, graph=False, fused_lmhead=fused)
+        probe.enabled = True
+        for i in range(steps):
+            params, state, loss = eager(params, state, batches[i % 4])
+        torch.cuda.synchronize()
+    probe.enabled = False
+    # The same step once more on one stream (no weight-gradient overlap): every
+    # kernel alone on the GPU, its own speed without CUs shared with the other
+    # stream.
+    iso_probe = KernelProbe(torch)
+    _lib.set_probe(iso_probe)
+    solo = make_train_step(opt, cfg, graph=False, fused_lmhead=fused, overlap_wgrad=False)
+    iso_steps = min(steps, 5)
+    iso_probe.enabled = True
+    for i in range(iso_steps):
+        params, state, loss = solo(params, state, batches[i % 4])
+    torch.cuda.synchronize()
+    iso_probe.enabled = False
+    _lib.set_probe(None)
+    fl = flops_per_step(cfg, bs, seq)
+    res = {"value": bs * seq * steps / dt, "ms": dt / steps * 1e3, "steps": steps,
+           "kernels": probe.summary(steps), "iso": iso_probe.summary(iso_steps),
+           "mfu": round(fl["total"] / (dt / steps) / (PEAK_BF16_TFLOPS * 1e12), 4),
+           "tflop": round(fl["total"] / 1e12, 4),
+           "six_n_t_tflops": round(fl["six_n_t"] / (dt / steps) / 1e12, 2),
+           "peak_hbm_gib": round(peak / 2**30, 2), "loss": round(float(loss.detach()), 4)}
+    del params, state, step, eager, solo, batches, loss, opt, probe, iso_probe
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return res
 
 
 if __name__ == "__main__":

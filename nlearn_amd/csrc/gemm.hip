@@ -1165,20 +1165,35 @@ template __global__ void gemm2_kernel<256, 128, 32, 2, false, false, uint16_t, N
 // beta*C for the degenerate K == 0 case is handled by the main kernel (nk = 0).
 
 // C = epilogue(alpha * s * sum_split ws[split]), summed in split order (deterministic).
+// Block = 64 column groups of 4 x 4 rows; grid (ceil(N/256), min(ceil(M/4), 65535)),
+// rows strided by the grid. The partials of one group are loaded 8 splits at a
+// time with every load in flight before the first add (the adds stay in split
+// order), so a thread waits for one memory latency per 8 splits, not per split.
 template <typename OutT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g, int splits) {
-  const int64_t groups_n = (g.N + 3) / 4;
-  const int64_t total = (int64_t)g.M * groups_n;
+  const int n = ((int)blockIdx.x * 64 + ((int)threadIdx.x & 63)) * 4;
+  if (n >= g.N) return;
   float s = g.alpha;
   if (g.alpha_dev) s *= *g.alpha_dev;
   const int64_t plane = (int64_t)g.M * g.ldw;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t m = i / groups_n;
-    const int n = (int)(i - m * groups_n) * 4;
+  for (int64_t m = (int64_t)blockIdx.y * 4 + ((int)threadIdx.x >> 6); m < g.M; m += (int64_t)gridDim.y * 4) {
     const float* w = g.ws + m * g.ldw + n;
-    f32x4 acc = *reinterpret_cast<const f32x4*>(w);
-    for (int sp = 1; sp < splits; ++sp) {
-      const f32x4 p = *reinterpret_cast<const f32x4*>(w + sp * plane);
+    f32x4 acc = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(w));
+    int sp = 1;
+    for (; sp + 8 <= splits; sp += 8) {
+      f32x4 p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(w + (sp + j) * plane));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        acc[0] += p[j][0];
+        acc[1] += p[j][1];
+        acc[2] += p[j][2];
+        acc[3] += p[j][3];
+      }
+    }
+    for (; sp < splits; ++sp) {
+      const f32x4 p = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(w + sp * plane));
       acc[0] += p[0];
       acc[1] += p[1];
       acc[2] += p[2];
@@ -1359,9 +1374,8 @@ void launch_cfg(GemmArgs g, const Plan& p, hipStream_t st) {
   if (p.splits > 1) {
     g.ldw = p.ldw;  // g.ws already set by the caller
     launch2(p.tiles * p.splits);
-    const int64_t work = (int64_t)g.M * ((g.N + 3) / 4);
-    const int blocks = (int)std::min<int64_t>((work + 255) / 256, 4096);
-    hipLaunchKernelGGL((splitk_reduce_kernel<OutT>), dim3(blocks), dim3(256), 0, st, g, p.splits);
+    const dim3 grid((unsigned)((g.N + 255) / 256), (unsigned)std::min<int64_t>(((int64_t)g.M + 3) / 4, 65535));
+    hipLaunchKernelGGL((splitk_reduce_kernel<OutT>), grid, dim3(256), 0, st, g, p.splits);
   } else {
     g.ws = nullptr;
     launch2(p.tiles);

@@ -111,6 +111,53 @@ def _gelu_bwd(du_out, u, t):
     return du_out * (0.5 * (1.0 + t) + 0.5 * u * dt)
 
 
+def _per_head(fn, bs: int, H: int) -> None:
+    """fn(b, h) for every head, on a thread pool (NumPy releases the GIL in
+    its array loops, so long sequences use every host core)."""
+    with cf_threads.ThreadPoolExecutor(max_workers=max(1, min(16, len(os.sched_getaffinity(0))))) as ex:
+        list(ex.map(lambda bh: fn(*bh), [(b, h) for b in range(bs) for h in range(H)]))
+
+
+def _attention_fwd(q, k, v, scale, mask):
+    """Materialised causal attention (attention.py:138-156), one head at a time:
+    P = softmax(scale * q k^T with the future masked to -inf), O = P v.
+    q, k, v: (bs, H, S, dh). Returns O and P (kept for the backward)."""
+    bs, H, S, _ = q.shape
+    o = np.empty_like(q)
+    pr = np.empty((bs, H, S, S), dtype=q.dtype)
+
+    def head(b, h):
+        s = (q[b, h] @ k[b, h].T) * scale
+        s[mask] = -np.inf
+        s -= s.max(-1, keepdims=True)
+        p = np.exp(s, out=s)
+        p /= p.sum(-1, keepdims=True)
+        pr[b, h] = p
+        o[b, h] = p @ v[b, h]
+
+    _per_head(head, bs, H)
+    return o, pr
+
+
+def _attention_bwd(q, k, v, pr, do, scale):
+    """Analytic backward of _attention_fwd (validate_flash_bwd.py:31-38):
+    dV = P^T dO, dP = dO V^T, dS = P (dP - rowsum(dP P)), dQ = scale dS K,
+    dK = scale dS^T Q; one head at a time."""
+    bs, H = q.shape[:2]
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+
+    def head(b, h):
+        p = pr[b, h]
+        dv[b, h] = p.T @ do[b, h]
+        dp = do[b, h] @ v[b, h].T
+        ds = p * (dp - (dp * p).sum(-1, keepdims=True))
+        dq[b, h] = (ds @ k[b, h]) * scale
+        dk[b, h] = (ds.T @ q[b, h]) * scale
+
+    _per_head(head, bs, H)
+    return dq, dk, dv
+
+
 def loss_and_grads(params, batch, cfg: Config = BASELINE, exact: bool = False, grads: bool = True):
     """Mean next-token CE of a (bs, seq+1) batch and the gradient of every parameter.
 
@@ -139,12 +186,7 @@ def loss_and_grads(params, batch, cfg: Config = BASELINE, exact: bool = False, g
         h = bf16_round(h)
         qkv = bf16_round(_mm(h.reshape(-1, d), blk["attn"]["W_qkv"])).reshape(bs, S, 3, H, dh)
         q, k, v = (np.ascontiguousarray(qkv[:, :, i].transpose(0, 2, 1, 3)) for i in range(3))
-        s = (q @ k.transpose(0, 1, 3, 2)) * scale
-        s = np.where(mask, -np.inf, s)
-        s = s - s.max(-1, keepdims=True)
-        pr = np.exp(s)
-        pr /= pr.sum(-1, keepdims=True)
-        o = pr @ v
+        o, pr = _attention_fwd(q, k, v, scale, mask)
         a = bf16_round(o.transpose(0, 2, 1, 3).reshape(bs, S, d))
         x1 = bf16_round(x + bf16_round(_mm(a.reshape(-1, d), blk["attn"]["W_o"])).reshape(bs, S, d))
         h2, c["ln2"] = _ln_fwd(x1, blk["ln2"]["gamma"], blk["ln2"]["beta"], cfg.eps)
@@ -214,11 +256,7 @@ def loss_and_grads(params, batch, cfg: Config = BASELINE, exact: bool = False, g
         gb["attn"]["W_o"] = c["a"].reshape(-1, d).T @ bf16_round(dyo)
         da = (bf16_round(dyo) @ bf16_round(blk["attn"]["W_o"]).T).reshape(bs, S, H, dh).transpose(0, 2, 1, 3)
         pr, q, k, v = c["pr"], c["q"], c["k"], c["v"]
-        dv = pr.transpose(0, 1, 3, 2) @ da
-        dp = da @ v.transpose(0, 1, 3, 2)
-        ds = pr * (dp - (dp * pr).sum(-1, keepdims=True))
-        dq = (ds @ k) * scale
-        dk = (ds.transpose(0, 1, 3, 2) @ q) * scale
+        dq, dk, dv = _attention_bwd(q, k, v, pr, np.ascontiguousarray(da), scale)
         dqkv = np.stack([t_.transpose(0, 2, 1, 3) for t_ in (dq, dk, dv)], axis=2).reshape(-1, 3 * d)
         gb["attn"]["W_qkv"] = c["h"].reshape(-1, d).T @ bf16_round(dqkv)
         dh1 = (bf16_round(dqkv) @ bf16_round(blk["attn"]["W_qkv"]).T).reshape(bs, S, d)

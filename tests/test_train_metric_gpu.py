@@ -5,6 +5,9 @@
   weight-gradient stream and the deferred LayerNorm sums on (as in the bench),
   then two more steps through the captured HIP graph; through both loss paths
   (LM head + CE, and linear_cross_entropy). Constant lr 1e-3 (the peak lr).
+* configs[4]'s variant at its own batch, bs4 x seq4096 (flash at (32, 4096,
+  64) per layer, a 4096-row position table): the same three steps, run the way
+  bench.py --batch-size 4 --seq-len 4096 runs them, through both loss paths.
 * configs[0] with the baseline's parity companion run: bs4 x seq512, AdamW lr 3e-4,
   a 20-step loss curve through the HIP graph from the same initial weights
   and batches as the oracle.
@@ -32,35 +35,52 @@ def bs32_oracle():
     """Three oracle steps at bs32 x seq512: losses, and step 1's gradients."""
     rng = np.random.default_rng(3232)
     batches = [rng.integers(0, 50257, (32, 513)).astype(np.int32) for _ in range(3)]
-    params = om.init_params(0)
+    return _three_oracle_steps(batches, om.BASELINE, "bs32")
+
+
+def _three_oracle_steps(batches, ocfg, tag):
+    """Oracle losses of three AdamW steps (constant lr LR32) from init_params(0)
+    and the first step's gradients."""
+    params = om.init_params(0, ocfg)
     opt = om.AdamWNP(params, lambda c: LR32)
-    print("oracle bs32 step 1", flush=True)
-    loss1, g1 = om.loss_and_grads(params, batches[0].astype(np.int64))
+    print(f"oracle {tag} step 1", flush=True)
+    loss1, g1 = om.loss_and_grads(params, batches[0].astype(np.int64), ocfg)
     opt.step(params, g1)
-    print("oracle bs32 step 2", flush=True)
-    loss2, g2 = om.loss_and_grads(params, batches[1].astype(np.int64))
+    print(f"oracle {tag} step 2", flush=True)
+    loss2, g2 = om.loss_and_grads(params, batches[1].astype(np.int64), ocfg)
     opt.step(params, g2)
     del g2
-    print("oracle bs32 step 3 (forward)", flush=True)
-    loss3, _ = om.loss_and_grads(params, batches[2].astype(np.int64), grads=False)
+    print(f"oracle {tag} step 3 (forward)", flush=True)
+    loss3, _ = om.loss_and_grads(params, batches[2].astype(np.int64), ocfg, grads=False)
     return batches, [loss1, loss2, loss3], g1
 
 
-@pytest.mark.timeout(900)
-@pytest.mark.parametrize("fused", [False, True], ids=["linear+ce", "linear_cross_entropy"])
-def test_metric_config_bs32_step_matches_oracle(dev, bs32_oracle, fused):
+@pytest.fixture(scope="module")
+def bs4_seq4096_oracle():
+    """Three oracle steps at bs4 x seq4096 (about 20 GB of host memory: the
+    oracle keeps every layer's (4, 8, 4096, 4096) attention probabilities)."""
+    rng = np.random.default_rng(4444)
+    batches = [rng.integers(0, 50257, (4, 4097)).astype(np.int32) for _ in range(3)]
+    return _three_oracle_steps(batches, om.Config(max_seq=4096), "bs4xseq4096")
+
+
+def _device_three_steps(dev, oracle, fused, cfg, tag):
+    """The bench's step (HIP graph after one eager step, weight-gradient
+    stream and deferred LayerNorm sums on) against three oracle steps: loss at
+    every step within 1e-2, and after the eager first step every parameter
+    gradient in main_grad within rel-L2 5e-2."""
     import torch
     from nlearn_amd.model import init_model, tree_leaves
     from nlearn_amd.train import AdamW, make_train_step
 
-    batches, ref_losses, g1 = bs32_oracle
+    batches, ref_losses, g1 = oracle
     opt = AdamW(lambda c: LR32)
-    params = init_model(0, device=dev)
+    params = init_model(0, cfg, dev)
     state = opt.init(params)
-    step = make_train_step(opt, graph=True, warmup=1, fused_lmhead=fused)
+    step = make_train_step(opt, cfg, graph=True, warmup=1, fused_lmhead=fused)
     got = []
     for i, b in enumerate(batches):
-        print(f"device bs32 step {i + 1} fused={fused}", flush=True)
+        print(f"device {tag} step {i + 1} fused={fused}", flush=True)
         params, state, loss = step(params, state, torch.from_numpy(b).to(dev))
         got.append(loss.item())
         if i == 0:  # the eager step: main_grad now holds step 1's gradients
@@ -69,6 +89,22 @@ def test_metric_config_bs32_step_matches_oracle(dev, bs32_oracle, fused):
                 assert err < 5e-2, (name, err)
     print("device", np.round(got, 5).tolist(), "oracle", np.round(ref_losses, 5).tolist())
     assert np.abs(np.array(got) - np.array(ref_losses)).max() < 1e-2
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("fused", [False, True], ids=["linear+ce", "linear_cross_entropy"])
+def test_metric_config_bs32_step_matches_oracle(dev, bs32_oracle, fused):
+    from nlearn_amd.model import BASELINE
+
+    _device_three_steps(dev, bs32_oracle, fused, BASELINE, "bs32")
+
+
+@pytest.mark.timeout(1200)
+@pytest.mark.parametrize("fused", [False, True], ids=["linear+ce", "linear_cross_entropy"])
+def test_configs4_bs4_seq4096_step_matches_oracle(dev, bs4_seq4096_oracle, fused):
+    from nlearn_amd.model import ModelConfig
+
+    _device_three_steps(dev, bs4_seq4096_oracle, fused, ModelConfig(max_seq_len=4096), "bs4xseq4096")
 
 
 @pytest.mark.timeout(900)
