@@ -215,10 +215,25 @@ def _cpu_model() -> str:
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
 
 
+# The products --traffic-probe runs, in launch order within one repetition:
+# (tag, M, N, K, algorithmic bytes). The LM head's three GEMMs, then the four
+# layer weight-gradient products X^T dY at M = 16384 tokens (fp32 outputs, K
+# split into fp32 partials that a second kernel reduces).
+def _traffic_products():
+    T, d, f, V = 16384, 512, 2048, 50257
+    prods = [("gemm_NN_16384x50257x512", 2 * (T * d + d * V + T * V)),
+             ("gemm_NT_16384x512x50257", 2 * (T * V + d * V + T * d)),
+             ("gemm_TN_512x50257x16384", 2 * (T * d + T * V) + 4 * d * V)]
+    for kin, nout in ((d, 3 * d), (d, d), (d, f), (f, d)):
+        prods.append((f"gemm_TN_{kin}x{nout}x{T}", 2 * (T * kin + T * nout) + 4 * kin * nout))
+    return prods
+
+
 def traffic_probe(reps: int = 5) -> None:
-    """The LM-head GEMMs alone at the bench shapes (forward NN, input-gradient NT
-    with its K split and reduction, weight-gradient TN), on inputs with the
-    training step's statistics, and a plain 1 GiB device copy: the known-size
+    """The LM-head GEMMs (forward NN, input-gradient NT with its K split and
+    reduction, weight-gradient TN) and the layer weight-gradient TN products
+    alone at the bench shapes, on inputs with the training step's statistics,
+    each repetition ending with a plain 1 GiB device copy: the known-size
     reference that calibrates the PMC byte counters."""
     import torch
 
@@ -235,52 +250,68 @@ def traffic_probe(reps: int = 5) -> None:
     y = padded_empty(M, N, torch.bfloat16, dev)
     dx = padded_empty(M, K, torch.bfloat16, dev)
     dw = padded_empty(K, N, torch.float32, dev)
+    layer = []
+    for kin, nout in ((512, 1536), (512, 512), (512, 2048), (2048, 512)):
+        a = padded_empty(M, kin, torch.bfloat16, dev)
+        a.copy_(torch.randn((M, kin), device=dev, generator=g))
+        dy = padded_empty(M, nout, torch.bfloat16, dev)
+        dy.copy_(torch.randn((M, nout), device=dev, generator=g))
+        layer.append((a, dy, torch.empty((kin, nout), dtype=torch.float32, device=dev)))
     src = torch.ones(2**28, dtype=torch.float32, device=dev)   # 1 GiB
     dst = torch.empty_like(src)
     for _ in range(reps):
         gemm_raw(x, w, out=y)                 # logits = x W
         gemm_raw(y, w, "N", "T", out=dx)      # dX = dlogits W^T
         gemm_raw(x, y, "T", "N", out=dw)      # dW = x^T dlogits
+        for a, dy, out in layer:              # the layers' X^T dY
+            gemm_raw(a, dy, "T", "N", out=out)
         dst.copy_(src)
     torch.cuda.synchronize()
-    print(json.dumps({"probe": "traffic", "shape": [M, N, K], "copy_bytes": 2**30, "reps": reps}))
+    print(json.dumps({"probe": "traffic", "products": [t for t, _ in _traffic_products()], "copy_bytes": 2**30,
+                      "reps": reps}))
 
 
-def _probe_kernel_tag(name: str):
-    """bench.py tag of a kernel dispatched by --traffic-probe (None for others).
-    GEMM layouts are told apart by the A/B k-major template arguments."""
-    if "copyBuffer" in name:
-        return "copy"
-    if "splitk_reduce_kernel" in name:
-        return "gemm_NT_16384x512x50257"      # the only split product of the probe
-    if "gemm" in name and "<" in name:
-        args = [t.strip() for t in name.split("<", 1)[1].split(",")]
-        # gemm2_kernel<BM, BN, BKT, S, A_KMAJ, B_KMAJ, ...>, gemm_persist_kernel<A_KMAJ, B_KMAJ, ...>
-        layout = (args[0], args[1]) if "persist" in name else (args[4], args[5]) if len(args) >= 6 else None
-        if layout:
-            return {("true", "false"): "gemm_NN_16384x50257x512", ("true", "true"): "gemm_NT_16384x512x50257",
-                    ("false", "false"): "gemm_TN_512x50257x16384"}.get(layout)
-    return None
+def _probe_dispatch_tags(names):
+    """bench.py tags of the dispatches of --traffic-probe, given their kernel
+    names in dispatch order: the GEMM kernels take the products' tags in launch
+    order (cycling per repetition), a split-K reduction the tag of the GEMM
+    before it, the 1 GiB copy "copy"; anything else (set-up) None."""
+    order = [t for t, _ in _traffic_products()]
+    tags, i, last = [], 0, None
+    for n in names:
+        if "copyBuffer" in n:
+            tags.append("copy")
+        elif "splitk_reduce_kernel" in n:
+            tags.append(last)
+        elif ("gemm2_kernel" in n or "gemm_persist_kernel" in n) and "<" in n:
+            last = order[i % len(order)]
+            i += 1
+            tags.append(last)
+        else:
+            tags.append(None)
+    return tags
 
 
 def traffic_summary(fetch_dir: str, write_dir: str) -> None:
     """HBM bytes per launch of the probe's GEMMs from two rocprofv3 --pmc runs:
     each counter's median over the probe's repetitions, summed over the kernels
-    of one product (the split NT adds its reduction), scaled by what the same
-    counter reads for the 1 GiB copy (known bytes)."""
+    of one product (a split product adds its reduction), scaled by what the
+    same counter reads for the 1 GiB copy (known bytes)."""
     import csv
     import glob
     import statistics
 
     def read(d, counter):
-        per = {}          # tag -> kernel name -> [KiB per dispatch]
+        rows = []
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
             for r in csv.DictReader(open(f)):
-                if r["Counter_Name"] != counter:
-                    continue
-                tag = _probe_kernel_tag(r["Kernel_Name"])
-                if tag:
-                    per.setdefault(tag, {}).setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+        rows.sort()
+        per = {}          # tag -> kernel name -> [KiB per dispatch]
+        for (_, name, val), tag in zip(rows, _probe_dispatch_tags([r[1] for r in rows])):
+            if tag:
+                per.setdefault(tag, {}).setdefault(name, []).append(val)
         return {t: {k: statistics.median(v) for k, v in ks.items()} for t, ks in per.items()}
 
     fetch, write = read(fetch_dir, "FETCH_SIZE"), read(write_dir, "WRITE_SIZE")
@@ -288,10 +319,6 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
     cf = sum(fetch["copy"].values())
     cw = sum(write["copy"].values())
     fs, ws = copy_bytes / (cf * 1024), copy_bytes / (cw * 1024)
-    M, N, K = 16384, 50257, 512
-    algo = {"gemm_NN_16384x50257x512": 2 * (M * K + K * N + M * N),
-            "gemm_NT_16384x512x50257": 2 * (M * N + K * N + M * K),
-            "gemm_TN_512x50257x16384": 2 * (M * K + M * N) + 4 * K * N}
     out = {"calibration": {"kernel": "__amd_rocclr_copyBuffer (torch copy_ of 1 GiB fp32)", "bytes": copy_bytes,
                            "fetch_kib_raw": cf, "write_kib_raw": cw, "fetch_scale": round(fs, 4),
                            "write_scale": round(ws, 4)},
@@ -301,11 +328,13 @@ def traffic_summary(fetch_dir: str, write_dir: str) -> None:
                         "python3 <repo>/bench.py --traffic-probe",
                         "python3 bench.py --traffic-summary <fetch> <write>"],
            "kernels": {}}
-    for tag, a in algo.items():
+    for tag, a in _traffic_products():
         fk, wk = sum(fetch.get(tag, {}).values()), sum(write.get(tag, {}).values())
         fb, wb = int(fk * 1024 * fs), int(wk * 1024 * ws)
         out["kernels"][tag] = {"dispatch_kernels": sorted(fetch.get(tag, {})), "fetch_kib_raw": fk,
                                "write_kib_raw": wk, "fetch_bytes": fb, "write_bytes": wb,
+                               "per_kernel_fetch_kib_raw": fetch.get(tag, {}),
+                               "per_kernel_write_kib_raw": write.get(tag, {}),
                                "bytes_per_launch": fb + wb, "algorithmic_bytes": a,
                                "traffic_over_algorithmic": round((fb + wb) / a, 3)}
     with open(TRAFFIC_FILE, "w") as f:

@@ -117,3 +117,31 @@ def test_graceful_stop_turns_sigterm_and_sigint_into_a_flag():
             os.kill(os.getpid(), sig)   # the Python-level handler runs before the next bytecode
             assert stop.requested
         assert {s: signal.getsignal(s) for s in before} == before
+
+
+def test_traffic_probe_dispatch_attribution():
+    """--traffic-summary attributes PMC rows by dispatch order: GEMM kernels
+    take the probe's product tags in launch order (cycling per repetition), a
+    split-K reduction joins the GEMM before it, the copy is the calibration,
+    and set-up kernels are ignored."""
+    import bench
+
+    order = [t for t, _ in bench._traffic_products()]
+    assert order[:3] == ["gemm_NN_16384x50257x512", "gemm_NT_16384x512x50257", "gemm_TN_512x50257x16384"]
+    assert len(order) == 7 and len(set(order)) == 7
+    rep = ["void nl::gemm_persist_kernel<true, false, unsigned short, 256, 256, 8, 0>(x)",
+           "void nl::gemm2_kernel<256, 256, 64, 2, true, true, unsigned short, 0>(x)",
+           "void nl::splitk_reduce_kernel<unsigned short>(x)",
+           "void nl::gemm2_kernel<256, 256, 64, 2, false, false, float, 0>(x)"]
+    for _ in range(4):
+        rep += ["void nl::gemm2_kernel<128, 128, 64, 2, false, false, float, 0>(x)",
+                "void nl::splitk_reduce_kernel<float>(x)"]
+    rep.append("__amd_rocclr_copyBuffer")
+    names = ["at::native::normal_kernel(x)"] + rep + rep
+    tags = bench._probe_dispatch_tags(names)
+    assert tags[0] is None
+    one = tags[1:1 + len(rep)]
+    assert one == tags[1 + len(rep):]
+    assert one[:4] == [order[0], order[1], order[1], order[2]]
+    assert one[4:12] == [t for t in order[3:] for _ in range(2)]
+    assert one[-1] == "copy"
