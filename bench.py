@@ -221,9 +221,11 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
 # split into fp32 partials that a second kernel reduces).
 def _traffic_products():
     T, d, f, V = 16384, 512, 2048, 50257
+    h = T // 2   # the training step's logits GEMM runs in two row chunks
     prods = [("gemm_NN_16384x50257x512", 2 * (T * d + d * V + T * V)),
              ("gemm_NT_16384x512x50257", 2 * (T * V + d * V + T * d)),
-             ("gemm_TN_512x50257x16384", 2 * (T * d + T * V) + 4 * d * V)]
+             ("gemm_TN_512x50257x16384", 2 * (T * d + T * V) + 4 * d * V),
+             (f"gemm_NN_{h}x50257x512", 2 * (h * d + d * V + h * V))]
     for kin, nout in ((d, 3 * d), (d, d), (d, f), (f, d)):
         prods.append((f"gemm_TN_{kin}x{nout}x{T}", 2 * (T * kin + T * nout) + 4 * kin * nout))
     return prods
@@ -263,6 +265,7 @@ def traffic_probe(reps: int = 5) -> None:
         gemm_raw(x, w, out=y)                 # logits = x W
         gemm_raw(y, w, "N", "T", out=dx)      # dX = dlogits W^T
         gemm_raw(x, y, "T", "N", out=dw)      # dW = x^T dlogits
+        gemm_raw(x[:M // 2], w, out=y[:M // 2])   # one of the step's two logits chunks
         for a, dy, out in layer:              # the layers' X^T dY
             gemm_raw(a, dy, "T", "N", out=out)
         dst.copy_(src)

@@ -440,9 +440,11 @@ int nl_embedding_fwd(void* stream, int batch, int seq, int D, int vocab, const i
  * [vocab][D] table: rows no token uses are written as zero, so dtok needs no
  * zeroing first. dpos[s] (+)= sum_b dx[b][s] in batch order for s < seq (rows of
  * dpos at or past seq are not touched). D % 4 == 0, D <= 4096; dtok 16-byte and
- * dx 8-byte aligned. Two launches (the positions of each vocabulary bucket
- * listed in token order, then the rows) over a workspace of
- * nl_embedding_bwd_ws_bytes() bytes, 16-byte aligned (unused with no tokens).
+ * dx 8-byte aligned. Three launches (the tokens of each vocabulary bucket
+ * counted, then listed in token order, then the rows) over a workspace of
+ * nl_embedding_bwd_ws_bytes() bytes, 16-byte aligned (unused with no tokens):
+ * one 8-byte entry per token plus 32 bytes per vocabulary bucket (at most 256
+ * buckets).
  * The autodiff of the gather in model.py:75-85. */
 size_t nl_embedding_bwd_ws_bytes(int batch, int seq, int D, int vocab);
 int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,

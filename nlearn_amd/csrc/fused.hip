@@ -376,14 +376,20 @@ __global__ __launch_bounds__(128) void embed_fwd_kernel(int S, int D, const int3
   }
 }
 
-// The embedding backward, deterministic and without atomics, in two launches.
+// The embedding backward, deterministic (no floating-point atomics), in three
+// launches over a workspace of exactly one 8-byte entry per token:
 //
-// embed_bucket_kernel: workgroup (b, k) owns the vocabulary rows
-// [b W, b W + W) (a bucket) and the k-th of P equal ranges of token positions.
-// It scans its range in order, appending (t, ids[t]) for the positions whose
-// id falls in its rows to its own segment lists[b][k][0, counts[b][k])
-// (capacity the range's length), so each segment is in increasing t and the
-// segments of a bucket in order are too. Ids outside [0, vocab) go nowhere.
+// embed_count_kernel: workgroup k counts, for each bucket b of W vocabulary
+// rows [b W, b W + W), the positions of the k-th of P equal token ranges whose
+// id falls in it: counts[b][k] (integer counts; the order of the LDS
+// increments does not change them). Ids outside [0, vocab) go nowhere.
+//
+// embed_bucket_kernel: workgroup (b, k) appends, in increasing t, the (t,
+// ids[t]) of its range whose id falls in bucket b to its segment of the list,
+// which starts at the number of entries of every (b', k') before (b, k) in
+// (bucket, range) order, and records that start in offsets[b][k]. The segments
+// of a bucket are then contiguous and in increasing t, and the lists hold
+// exactly the valid tokens.
 //
 // embed_bwd_kernel (one wave per workgroup):
 // * workgroups [0, S) form dpos[s] (+)= sum_b dx[b, s] in batch order;
@@ -395,6 +401,7 @@ __global__ __launch_bounds__(128) void embed_fwd_kernel(int S, int D, const int3
 constexpr int kEmbTokLds = 16384;  // bytes of LDS per row workgroup (R = 16384 / (4 D) rows)
 constexpr int kEmbBuckets = 256;   // target number of buckets
 constexpr int kEmbParts = 4;       // token ranges per bucket (one scanning workgroup each)
+constexpr int kEmbMaxBuckets = 256;  // W = ceil(vocab / 256) rounded up to R: at most 256 buckets
 
 struct EmbPlan {
   int R;        // token-table rows per row workgroup
@@ -412,8 +419,25 @@ EmbPlan emb_plan(int D, int vocab) {
   return p;
 }
 
+__global__ __launch_bounds__(256) void embed_count_kernel(int T, int vocab, int W, int buckets,
+                                                          const int32_t* __restrict__ ids, int* __restrict__ counts) {
+  __shared__ int hist[kEmbMaxBuckets];
+  const int tid = threadIdx.x, k_part = blockIdx.x;
+  for (int b = tid; b < buckets; b += 256) hist[b] = 0;
+  __syncthreads();
+  const int span = (T + kEmbParts - 1) / kEmbParts;
+  const int t0 = k_part * span, t1 = min(T, t0 + span);
+  for (int t = t0 + tid; t < t1; t += 256) {
+    const int id = ids[t];
+    if ((uint32_t)id < (uint32_t)vocab) atomicAdd(&hist[id / W], 1);
+  }
+  __syncthreads();
+  for (int b = tid; b < buckets; b += 256) counts[b * kEmbParts + k_part] = hist[b];
+}
+
 __global__ __launch_bounds__(256) void embed_bucket_kernel(int T, int vocab, int W, const int32_t* __restrict__ ids,
-                                                           int* __restrict__ counts, int2* __restrict__ lists) {
+                                                           const int* __restrict__ counts, int* __restrict__ offsets,
+                                                           int2* __restrict__ lists) {
   __shared__ int wave_tot[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int b = blockIdx.x / kEmbParts, k_part = blockIdx.x % kEmbParts;
@@ -421,7 +445,17 @@ __global__ __launch_bounds__(256) void embed_bucket_kernel(int T, int vocab, int
   const int nrows = min(W, vocab - v0);
   const int span = (T + kEmbParts - 1) / kEmbParts;
   const int t0 = k_part * span, t1 = min(T, t0 + span);
-  int2* list = lists + (int64_t)b * T + t0;  // the segment: span entries from t0
+  // start of this segment: the entries of every (bucket, range) before it
+  int before = 0;
+  for (int i = tid; i < (int)blockIdx.x; i += 256) before += counts[i];
+#pragma unroll
+  for (int d = 32; d > 0; d >>= 1) before += __shfl_xor(before, d, 64);
+  if (lane == 0) wave_tot[wave] = before;
+  __syncthreads();
+  const int seg0 = wave_tot[0] + wave_tot[1] + wave_tot[2] + wave_tot[3];
+  if (tid == 0) offsets[blockIdx.x] = seg0;
+  __syncthreads();  // wave_tot is reused below
+  int2* list = lists + seg0;
   int cursor = 0;
   // thread tid holds positions c0 + 4 tid + e: in t order thread by thread, e
   // within; the next chunk's ids are loaded before this chunk is placed
@@ -465,12 +499,12 @@ __global__ __launch_bounds__(256) void embed_bucket_kernel(int T, int vocab, int
 #pragma unroll
     for (int e = 0; e < 4; ++e) cur[e] = nxt[e];
   }
-  if (tid == 0) counts[blockIdx.x] = cursor;  // counts[b][k]
 }
 
 __global__ __launch_bounds__(64) void embed_bwd_kernel(int B, int S, int D, const int32_t* __restrict__ ids,
                                                        const uint16_t* __restrict__ dx, float* __restrict__ dtok,
                                                        int vocab, int R, int W, const int* __restrict__ counts,
+                                                       const int* __restrict__ offsets,
                                                        const int2* __restrict__ lists, float* __restrict__ dpos,
                                                        int accumulate) {
   const int lane = threadIdx.x;
@@ -494,11 +528,10 @@ __global__ __launch_bounds__(64) void embed_bwd_kernel(int B, int S, int D, cons
   for (int i = lane; i < n4; i += 64) emb_acc4[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   __syncthreads();
   const int b = v0 / W;
-  const int span = (T + kEmbParts - 1) / kEmbParts;
   // the bucket's segments in order: every position of segment k precedes those of k + 1
   for (int kp = 0; kp < (T > 0 ? kEmbParts : 0); ++kp) {
     const int n = counts[b * kEmbParts + kp];
-    const int2* list = lists + (int64_t)b * T + (int64_t)kp * span;
+    const int2* list = lists + offsets[b * kEmbParts + kp];
     for (int j0 = 0; j0 < n; j0 += 64) {
       const int2 e = j0 + lane < n ? list[j0 + lane] : int2{0, -1};
       const int t = e.x, id = e.y;
@@ -723,11 +756,14 @@ extern "C" int nl_embedding_fwd(void* stream, int batch, int seq, int D, int voc
   return nl_check_launch("nl_embedding_fwd");
 }
 
+// counts and segment offsets ([buckets][parts] ints each), then one 8-byte
+// (t, id) entry per token from a 16-byte boundary
+static size_t emb_head_bytes(const EmbPlan& p) { return ((size_t)p.buckets * kEmbParts * 2 * sizeof(int) + 15) / 16 * 16; }
+
 extern "C" size_t nl_embedding_bwd_ws_bytes(int batch, int seq, int D, int vocab) {
   if (batch <= 0 || seq <= 0 || D <= 0 || vocab <= 0) return 0;
   const EmbPlan p = emb_plan(D, vocab);
-  // counts, then 8-byte (t, id) entries from a 16-byte boundary
-  return ((size_t)p.buckets * kEmbParts * sizeof(int) + 15) / 16 * 16 + (size_t)p.buckets * batch * seq * sizeof(int2);
+  return emb_head_bytes(p) + (size_t)batch * seq * sizeof(int2);
 }
 
 extern "C" int nl_embedding_bwd(void* stream, int batch, int seq, int D, int vocab, const int32_t* ids,
@@ -747,18 +783,21 @@ extern "C" int nl_embedding_bwd(void* stream, int batch, int seq, int D, int voc
   const int T = (int)T64;
   hipStream_t st = (hipStream_t)stream;
   int* counts = nullptr;
+  int* offsets = nullptr;
   int2* lists = nullptr;
   if (T > 0) {
     if (!ws || ws_bytes < nl_embedding_bwd_ws_bytes(batch, seq, D, vocab) || ((uintptr_t)ws & 15) != 0)
       return nl_set_error(NL_EINVAL, "embedding_bwd: workspace below nl_embedding_bwd_ws_bytes()");
+    if (p.buckets > kEmbMaxBuckets) return nl_set_error(NL_EUNSUPPORTED, "embedding_bwd: too many buckets");
     counts = reinterpret_cast<int*>(ws);
-    lists = reinterpret_cast<int2*>(reinterpret_cast<char*>(ws) +
-                                    ((size_t)p.buckets * kEmbParts * sizeof(int) + 15) / 16 * 16);
+    offsets = counts + (size_t)p.buckets * kEmbParts;
+    lists = reinterpret_cast<int2*>(reinterpret_cast<char*>(ws) + emb_head_bytes(p));
+    hipLaunchKernelGGL(embed_count_kernel, dim3(kEmbParts), dim3(256), 0, st, T, vocab, p.W, p.buckets, ids, counts);
     hipLaunchKernelGGL(embed_bucket_kernel, dim3(p.buckets * kEmbParts), dim3(256), 0, st, T, vocab, p.W, ids, counts,
-                       lists);
+                       offsets, lists);
   }
   // with no tokens every row of dtok is still written (zero): counts is not read then
   hipLaunchKernelGGL(embed_bwd_kernel, dim3((unsigned)(seq + p.groups)), dim3(64), p.R * D * 4, st, batch, seq, D,
-                     ids, dx, dtok, vocab, p.R, p.W, counts, lists, dpos, accumulate_pos);
+                     ids, dx, dtok, vocab, p.R, p.W, counts, offsets, lists, dpos, accumulate_pos);
   return nl_check_launch("nl_embedding_bwd");
 }

@@ -161,7 +161,7 @@ class _LMHeadCE(torch.autograd.Function):
     from dlogits scaled by the cotangent."""
 
     @staticmethod
-    def forward(ctx, x2, W, targets, chunks):
+    def forward(ctx, x2, W, targets, chunks, overlap):
         Wb = bf16_shadow(W)
         M, V = x2.shape[0], Wb.shape[1]
         t = _targets(targets)
@@ -174,7 +174,7 @@ class _LMHeadCE(torch.autograd.Function):
         lse = torch.empty(M, dtype=torch.float32, device=x2.device)
         main = torch.cuda.current_stream(x2.device)
         n = max(1, min(int(chunks), M))
-        aux = wgrad._side_stream(x2.device, 1) if n > 1 else None
+        aux = wgrad._side_stream(x2.device, 1) if n > 1 and overlap else None
         bounds = [M * i // n for i in range(n + 1)]
         for r0, r1 in zip(bounds[:-1], bounds[1:]):
             if r1 == r0:
@@ -183,7 +183,7 @@ class _LMHeadCE(torch.autograd.Function):
             ce = (lambda st, r0=r0, r1=r1: _lib.call(
                 "nl_ce_fwd_bwd", st, r1 - r0, V, logits[r0].data_ptr(), ld, t[r0].data_ptr(),
                 loss_rows[r0].data_ptr(), lse[r0].data_ptr(), 1.0 / M, logits[r0].data_ptr(), ld))
-            if n == 1:
+            if aux is None:
                 ce(main.cuda_stream)
                 continue
             # everything these CE launches touch was allocated above, on the
@@ -191,7 +191,7 @@ class _LMHeadCE(torch.autograd.Function):
             aux.wait_stream(main)
             with torch.cuda.stream(aux):
                 ce(aux.cuda_stream)
-        if n > 1:
+        if aux is not None:
             main.wait_stream(aux)
         ctx.save_for_backward(x2, W)
         ctx.wb = Wb
@@ -205,18 +205,20 @@ class _LMHeadCE(torch.autograd.Function):
         ctx.d = None
         scale_by_device_scalar_(d, g)
         dx, dW = linear_backward(x2, W, ctx.wb, d, ctx.needs_input_grad[0], ctx.needs_input_grad[1])
-        return dx, dW, None, None
+        return dx, dW, None, None, None
 
 
-def lm_head_cross_entropy(X: torch.Tensor, W: torch.Tensor, targets: torch.Tensor, chunks: int = 1) -> torch.Tensor:
+def lm_head_cross_entropy(X: torch.Tensor, W: torch.Tensor, targets: torch.Tensor, chunks: int = 1,
+                          overlap: bool = True) -> torch.Tensor:
     """Mean CE of logits = X . W (X [..., d] bf16, W [d, V]) against ``targets``,
     equal to ``cross_entropy(linear(X, W), targets, inplace=True)`` bit for
     bit; with ``chunks`` > 1 row chunks, the CE of one chunk overlaps the GEMM
-    of the next (see _LMHeadCE)."""
+    of the next (see _LMHeadCE) unless ``overlap`` is False (every kernel then
+    runs on the current stream, in the same order)."""
     if X.dim() < 2 or W.dim() != 2:
         raise ValueError("lm_head_cross_entropy: X needs >= 2 dims and W exactly 2")
     x2 = X.reshape(-1, X.shape[-1])
-    return _LMHeadCE.apply(x2, W, targets.reshape(-1), int(chunks))
+    return _LMHeadCE.apply(x2, W, targets.reshape(-1), int(chunks), bool(overlap))
 
 
 # ---------------------------------------------------------------------------

@@ -62,11 +62,14 @@ GRAD_CLIP = float(os.environ.get("NLEARN_GRAD_CLIP", "0"))
 # that the (bs*seq, vocab) logits are never materialised (train.py:24-28).
 FUSED_LMHEAD = os.environ.get("NLEARN_FUSED_LMHEAD") == "1"
 # row chunks of the LM head + CE on the default path (1: one GEMM, then one CE;
-# more: each chunk's CE beside the next chunk's GEMM, identical results)
-LMHEAD_CHUNKS = int(os.environ.get("NLEARN_LMHEAD_CHUNKS", "1"))
+# more: each chunk's CE beside the next chunk's GEMM, identical results). Two
+# measured fastest on MI355X at bs32 x seq512 (graph replays, 3 rounds on one
+# box: 5.98-6.00 ms with one chunk, 5.91-5.92 with two, 5.96 with four).
+LMHEAD_CHUNKS = int(os.environ.get("NLEARN_LMHEAD_CHUNKS", "2"))
 
 
-def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_lmhead: bool | None = None) -> torch.Tensor:
+def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_lmhead: bool | None = None,
+               overlap: bool = True) -> torch.Tensor:
     """Mean CE of predicting batch[:, 1:] from batch[:, :-1] (train.py:270-299).
 
     Default: the logits are only read by the CE, so its single pass writes
@@ -82,10 +85,11 @@ def batch_loss(params, batch: torch.Tensor, cfg: ModelConfig = BASELINE, fused_l
         x = model_forward_features(params, input_ids, cfg)
         return linear_cross_entropy(x.reshape(-1, cfg.d_model), output_projection(params), target_ids.reshape(-1))
     # logits = x . W_lm and the single-pass CE (dlogits over the logits), in
-    # LMHEAD_CHUNKS row chunks; the same values as
+    # LMHEAD_CHUNKS row chunks (each chunk's CE beside the next chunk's GEMM
+    # when ``overlap``); the same values as
     # cross_entropy(model_forward(...), targets, inplace=True)
     x = model_forward_features(params, input_ids, cfg)
-    return lm_head_cross_entropy(x, output_projection(params), target_ids, LMHEAD_CHUNKS)
+    return lm_head_cross_entropy(x, output_projection(params), target_ids, LMHEAD_CHUNKS, overlap)
 
 
 # ---------------------------------------------------------------------------
@@ -387,7 +391,9 @@ def make_train_step(optimizer, cfg: ModelConfig = BASELINE, graph: bool = False,
     optimizer's scalars are written to the device before each replay.
 
     overlap_wgrad: run the weight-gradient kernels on a second stream beside
-    the input-gradient chain (kernels.wgrad); results are identical.
+    the input-gradient chain (kernels.wgrad), and each LM-head chunk's CE
+    beside the next chunk's GEMM; results are identical. False runs every
+    kernel on the current stream.
 
     fused_lmhead: the loss through linear_cross_entropy (see ``batch_loss``).
     """
@@ -400,7 +406,7 @@ def make_train_step(optimizer, cfg: ModelConfig = BASELINE, graph: bool = False,
     def eager_step(params, opt_state, batch):
         for p in tree_leaves(params):
             p.grad = None
-        loss = batch_loss(params, batch, cfg, fused_lmhead)
+        loss = batch_loss(params, batch, cfg, fused_lmhead, overlap_wgrad)
         seed = None if scale == 1.0 else torch.full((), scale, dtype=torch.float32, device=loss.device)
         # weight gradients run on a second stream beside the dX chain; the
         # contexts join it and finish the LayerNorm parameter sums before the
@@ -473,7 +479,7 @@ class _GraphedStep:
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            loss = batch_loss(params, self.static_batch, self.cfg, self.fused_lmhead)
+            loss = batch_loss(params, self.static_batch, self.cfg, self.fused_lmhead, self.overlap is not _no_overlap)
             with self.overlap(loss.device), fused.defer_layer_norm_param_sums():
                 loss.backward(seed)
             with torch.no_grad():

@@ -273,12 +273,15 @@ def test_embedding_fwd_bwd(dev, B, S, V, D, P):
     assert np.array_equal(_np(posd.grad), dpos)
 
 
-def test_embedding_bwd_sums_in_token_order(dev):
+@pytest.mark.parametrize("pattern", ["skewed", "one_id", "all_outside"])
+def test_embedding_bwd_sums_in_token_order(dev, pattern):
     """Skewed ids (one id on a quarter of the tokens, a few hot ones, runs of
     the same id) and non-integer gradients, where the summation order shows in
     the last bits: the token table's gradient is np.add.at's float32 sum, in
     increasing token order, bit for bit; rows no token uses come back zero in
-    a table that started as NaN; ids outside [0, vocab) add nothing."""
+    a table that started as NaN; ids outside [0, vocab) add nothing. Also
+    every token on one id (one bucket's lists take the whole one-entry-per-
+    token workspace) and every id outside the table (empty lists)."""
     import torch
     from nlearn_amd import _lib
 
@@ -289,6 +292,10 @@ def test_embedding_bwd_sums_in_token_order(dev):
     ids[:, 100:140] = 2999
     ids[3, 7] = V
     ids[5, 9] = -4
+    if pattern == "one_id":
+        ids[:] = 1234
+    elif pattern == "all_outside":
+        ids[:] = V + rng.integers(0, 5, (B, S)).astype(np.int32)
     dx = ops.bf16_round(rng.standard_normal((B, S, D)).astype(np.float32))
     dtok = torch.full((V, D), float("nan"), device=dev)
     dpos = torch.zeros((S, D), device=dev)

@@ -128,11 +128,12 @@ def test_traffic_probe_dispatch_attribution():
 
     order = [t for t, _ in bench._traffic_products()]
     assert order[:3] == ["gemm_NN_16384x50257x512", "gemm_NT_16384x512x50257", "gemm_TN_512x50257x16384"]
-    assert len(order) == 7 and len(set(order)) == 7
+    assert len(order) == 8 and len(set(order)) == 8 and order[3] == "gemm_NN_8192x50257x512"
     rep = ["void nl::gemm_persist_kernel<true, false, unsigned short, 256, 256, 8, 0>(x)",
            "void nl::gemm2_kernel<256, 256, 64, 2, true, true, unsigned short, 0>(x)",
            "void nl::splitk_reduce_kernel<unsigned short>(x)",
-           "void nl::gemm2_kernel<256, 256, 64, 2, false, false, float, 0>(x)"]
+           "void nl::gemm2_kernel<256, 256, 64, 2, false, false, float, 0>(x)",
+           "void nl::gemm_persist_kernel<true, false, unsigned short, 256, 256, 8, 0>(x)"]
     for _ in range(4):
         rep += ["void nl::gemm2_kernel<128, 128, 64, 2, false, false, float, 0>(x)",
                 "void nl::splitk_reduce_kernel<float>(x)"]
@@ -142,6 +143,6 @@ def test_traffic_probe_dispatch_attribution():
     assert tags[0] is None
     one = tags[1:1 + len(rep)]
     assert one == tags[1 + len(rep):]
-    assert one[:4] == [order[0], order[1], order[1], order[2]]
-    assert one[4:12] == [t for t in order[3:] for _ in range(2)]
+    assert one[:5] == [order[0], order[1], order[1], order[2], order[3]]
+    assert one[5:13] == [t for t in order[4:] for _ in range(2)]
     assert one[-1] == "copy"

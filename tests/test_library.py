@@ -73,8 +73,9 @@ def test_status_strings_and_argument_errors_without_gpu():
     assert lib.nl_colsum_ws_bytes(16384, 2048) == 256 * 2048 * 4
     assert lib.nl_colsum_bf16(None, 8, 8, 256, 12, 512, 0, 768, 4096) == _lib.NL_EALIGN
     assert lib.nl_embedding_fwd(None, 2, 8, 6, 100, 256, 512, 768, 1024) == _lib.NL_EINVAL
-    # embedding backward: 252 buckets of 200 rows for the LM vocabulary at D = 512, 4 counts and T positions each
-    assert lib.nl_embedding_bwd_ws_bytes(32, 512, 512, 50257) == 4032 + 252 * 16384 * 8
+    # embedding backward: 252 buckets of 200 rows for the LM vocabulary at D = 512, 4 counts and 4 segment
+    # offsets each, then one (t, id) entry per token
+    assert lib.nl_embedding_bwd_ws_bytes(32, 512, 512, 50257) == 252 * 4 * 4 * 2 + 16384 * 8
     assert lib.nl_embedding_bwd_ws_bytes(0, 512, 512, 50257) == 0
     eargs = (None, 2, 8, 512, 100, 256, 512, 768, 1024, 0)
     assert lib.nl_embedding_bwd(*eargs, 1280, 16) == _lib.NL_EINVAL                    # workspace too small
@@ -222,3 +223,20 @@ def test_ctypes_table_matches_header_arity():
         params = " ".join(params.split())
         n = 0 if params in ("", "void") else params.count(",") + 1
         assert n == len(_lib._SIGNATURES[name]), (name, n, len(_lib._SIGNATURES[name]))
+
+
+def test_embedding_bwd_workspace_is_one_entry_per_token():
+    """The embedding backward's workspace holds one 8-byte (t, id) entry per
+    token plus the per-(bucket, range) counts and offsets: it grows with the
+    token count only, not with tokens x buckets (no GPU call)."""
+    from nlearn_amd import _lib
+
+    lib = _lib.load()
+    head = None
+    for B, S in ((32, 512), (4, 4096), (1, 1), (1024, 1024), (7, 333)):
+        b = int(lib.nl_embedding_bwd_ws_bytes(B, S, 512, 50257))
+        if head is None:
+            head = b - 8 * B * S
+        assert b == 8 * B * S + head
+    assert 0 < head <= 2 * 4 * 256 * 4 + 16     # two [buckets][4] int tables, <= 256 buckets
+    assert lib.nl_embedding_bwd_ws_bytes(0, 512, 512, 50257) == 0
