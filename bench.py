@@ -54,6 +54,9 @@ def _args():
     ap.add_argument("--replay-probe", action="store_true",
                     help="only warm up, capture and replay the graphed step --steps times (for rocprofv3 "
                          "--kernel-trace: the busy ratio of graph replays)")
+    ap.add_argument("--trace-summary", nargs="+", metavar="ARG",
+                    help="TRACE_DIR OUT.md TITLE COMMAND STEPS [BENCH_JSON KERNEL]: per-kernel table of a "
+                         "rocprofv3 --kernel-trace csv run, for profiles/")
     ap.add_argument("--busy-summary", metavar="TRACE_DIR",
                     help="write profiles/busy_<workload>.json from the rocprofv3 kernel trace of --replay-probe")
     ap.add_argument("--flash-probe", nargs=2, type=int, metavar=("N_HEADS", "SEQ"),
@@ -375,6 +378,69 @@ def busy_summary(trace_dir: str, steps: int, bs: int, seq: int) -> None:
         json.dump(out, f, indent=1)
     print(json.dumps({k: out[k] for k in ("wall_ms_per_step", "busy_union_ms_per_step", "busy_ratio",
                                           "kernel_sum_over_wall")}))
+
+
+def trace_summary(trace_dir: str, out_md: str, title: str, command: str, steps: int,
+                  bench_json: str | None = None, kernel: str | None = None) -> None:
+    """Markdown table of a rocprofv3 --kernel-trace (csv) run: per kernel, the
+    dispatches, time per step (``steps`` = steps the profiled command ran) and
+    the mean, median, min and max duration. With the bench line the profiled
+    run printed and the dominant kernel's name, the line's HIP-event mean is
+    set beside the kernel's rocprof mean."""
+    import csv
+    import glob
+    import statistics
+
+    rows = []
+    for f in glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            rows.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"]))
+    per = defaultdict(list)
+    for a, b, n in sorted(rows):
+        per[_kernel_short_name(n)].append((b - a) / 1e3)
+    total = sum(sum(v) for v in per.values())
+    lines = [f"# {title}", "", "Command (repository root of the GPU host, `TMPDIR=/tmp`):", "", "```", command, "```",
+             "", f"Kernel time of all {steps} steps the command runs (warm-up, timed, and bench.py's per-kernel "
+             f"passes): {total / steps / 1e3:.3f} ms per step.", ""]
+    if bench_json and kernel:
+        with open(bench_json) as f:
+            line = json.loads([l for l in f if l.startswith("{")][-1])
+        roof = line["roofline"]
+        d = per.get(kernel, [])
+        if d:
+            mean = statistics.mean(d)
+            lines += [f"Dominant kernel `{kernel}` (bench tag `{roof['kernel']}`): rocprof mean {mean:.1f} us over "
+                      f"{len(d)} dispatches (median {statistics.median(d):.1f}); the bench line of this run: "
+                      f"{roof['avg_us']:.1f} us in the step (frac {roof['frac']}), {roof['avg_us_isolated']:.1f} us "
+                      f"alone (frac {roof['frac_isolated']}), {line['ms_per_step']} ms per step, "
+                      f"{line['value'] / 1e6:.3f} M tokens/s.", ""]
+            # the same dispatches split by bench.py's passes, in launch order
+            lps = int(round(line["detail"]["kernels_in_step"][roof["kernel"]]["launches_per_step"]))
+            K, W = line["steps"], line["warmup"]
+            passes = [("warm-up and capture", max(W, 3)), ("timed graph replays", K),
+                      ("in-step pass (bench HIP events)", K), ("one-stream pass (alone)", min(K, 5))]
+            if "variant_bs4_seq4096" in line["detail"]:
+                vk, vw = min(K, 20), min(W, 5)
+                passes += [("variant warm-up", max(vw, 3)), ("variant replays", vk), ("variant in-step pass", vk),
+                           ("variant alone", min(vk, 5))]
+            if sum(n for _, n in passes) * lps == len(d):
+                lines += ["| pass | dispatches | rocprof mean us |", "|---|---:|---:|"]
+                i = 0
+                for name, n in passes:
+                    seg = d[i:i + n * lps]
+                    i += n * lps
+                    lines.append(f"| {name} | {len(seg)} | {statistics.mean(seg):.1f} |")
+                lines.append("")
+    lines += ["| ms / step | calls / step | mean us | median us | min us | max us | kernel |",
+              "|---:|---:|---:|---:|---:|---:|---|"]
+    for k, d in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        if sum(d) / steps < 1.0:   # below 1 us per step
+            continue
+        lines.append(f"| {sum(d) / steps / 1e3:.3f} | {len(d) / steps:.2f} | {statistics.mean(d):.1f} | "
+                     f"{statistics.median(d):.1f} | {min(d):.1f} | {max(d):.1f} | `{k}` |")
+    with open(out_md, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines[:14]))
 
 
 def busy_stats(rows, steps: int, bs: int, seq: int) -> dict:
@@ -701,6 +767,10 @@ def main():
         return
     if a.traffic_summary:
         traffic_summary(*a.traffic_summary)
+        return
+    if a.trace_summary:
+        t = a.trace_summary
+        trace_summary(t[0], t[1], t[2], t[3], int(t[4]), *(t[5:7]))
         return
     if a.busy_summary:
         busy_summary(a.busy_summary, a.steps, a.batch_size, a.seq_len)
