@@ -224,7 +224,9 @@ TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profile
 # split into fp32 partials that a second kernel reduces).
 def _traffic_products():
     T, d, f, V = 16384, 512, 2048, 50257
-    h = T // 2   # the training step's logits GEMM runs in two row chunks
+    from nlearn_amd.kernels.cross_entropy import chunk_bounds
+
+    h = chunk_bounds(T, 2)[1]   # the training step's logits GEMM runs in two row chunks; the first
     prods = [("gemm_NN_16384x50257x512", 2 * (T * d + d * V + T * V)),
              ("gemm_NT_16384x512x50257", 2 * (T * V + d * V + T * d)),
              ("gemm_TN_512x50257x16384", 2 * (T * d + T * V) + 4 * d * V),
@@ -255,6 +257,7 @@ def traffic_probe(reps: int = 5) -> None:
     y = padded_empty(M, N, torch.bfloat16, dev)
     dx = padded_empty(M, K, torch.bfloat16, dev)
     dw = padded_empty(K, N, torch.float32, dev)
+    h = int(_traffic_products()[3][0].split("_")[2].split("x")[0])
     layer = []
     for kin, nout in ((512, 1536), (512, 512), (512, 2048), (2048, 512)):
         a = padded_empty(M, kin, torch.bfloat16, dev)
@@ -268,7 +271,7 @@ def traffic_probe(reps: int = 5) -> None:
         gemm_raw(x, w, out=y)                 # logits = x W
         gemm_raw(y, w, "N", "T", out=dx)      # dX = dlogits W^T
         gemm_raw(x, y, "T", "N", out=dw)      # dW = x^T dlogits
-        gemm_raw(x[:M // 2], w, out=y[:M // 2])   # one of the step's two logits chunks
+        gemm_raw(x[:h], w, out=y[:h])         # the first of the step's two logits chunks
         for a, dy, out in layer:              # the layers' X^T dY
             gemm_raw(a, dy, "T", "N", out=out)
         dst.copy_(src)

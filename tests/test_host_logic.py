@@ -128,7 +128,7 @@ def test_traffic_probe_dispatch_attribution():
 
     order = [t for t, _ in bench._traffic_products()]
     assert order[:3] == ["gemm_NN_16384x50257x512", "gemm_NT_16384x512x50257", "gemm_TN_512x50257x16384"]
-    assert len(order) == 8 and len(set(order)) == 8 and order[3] == "gemm_NN_8192x50257x512"
+    assert len(order) == 8 and len(set(order)) == 8 and order[3] == "gemm_NN_9728x50257x512"
     rep = ["void nl::gemm_persist_kernel<true, false, unsigned short, 256, 256, 8, 0>(x)",
            "void nl::gemm2_kernel<256, 256, 64, 2, true, true, unsigned short, 0>(x)",
            "void nl::splitk_reduce_kernel<unsigned short>(x)",
@@ -146,3 +146,19 @@ def test_traffic_probe_dispatch_attribution():
     assert one[:5] == [order[0], order[1], order[1], order[2], order[3]]
     assert one[5:13] == [t for t in order[4:] for _ in range(2)]
     assert one[-1] == "copy"
+
+
+def test_lm_head_chunk_bounds():
+    """Row chunks of the LM head + CE: two chunks split at 60% of the rows in
+    whole 256-row tiles; other counts equal; always covering [0, M) in order."""
+    from nlearn_amd.kernels.cross_entropy import chunk_bounds
+
+    assert chunk_bounds(16384, 2) == [0, 9728, 16384]
+    assert chunk_bounds(16384, 1) == [0, 16384]
+    assert chunk_bounds(16384, 4) == [0, 4096, 8192, 12288, 16384]
+    assert chunk_bounds(300, 2) == [0, 150, 300]          # too short for whole tiles
+    assert chunk_bounds(3, 16) == [0, 1, 2, 3]
+    for M in (1, 255, 512, 777, 4096, 16385):
+        for n in (1, 2, 3, 7):
+            b = chunk_bounds(M, n)
+            assert b[0] == 0 and b[-1] == M and all(x <= y for x, y in zip(b, b[1:]))

@@ -8,7 +8,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("M,d,V,chunks,g", [(37, 64, 1000, 3, 1.0), (1024, 512, 5000, 4, 3.0),
-                                            (1000, 512, 50257, 7, 1.0), (16384, 512, 50257, 4, 1.0)])
+                                            (1000, 512, 50257, 7, 1.0), (16384, 512, 50257, 4, 1.0),
+                                            (16384, 512, 50257, 2, 2.0), (3000, 512, 50257, 2, 1.0)])
 def test_lm_head_cross_entropy_equals_linear_then_ce(dev, M, d, V, chunks, g):
     import torch
     from nlearn_amd.kernels.cross_entropy import cross_entropy, lm_head_cross_entropy
