@@ -531,7 +531,7 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   auto step = [&](uint16_t* cur, uint16_t* nxt, int kt) __attribute__((always_inline)) {
     wait_stage<IPS, S - 2>(min(S - 2, nfull - 1 - kt));
     if constexpr (S == 2) __syncthreads();
-    else asm volatile("s_barrier" ::: "memory");
+    else asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");  // this wave's LDS reads done
     if (kt + S - 1 < nfull) issue(nxt, kt + S - 1);
     compute(cur);
   };
@@ -968,8 +968,14 @@ __global__ __launch_bounds__(NWV * 64, NWV == 8 ? 1 : 2) void gemm_persist_kerne
     da.issue(ra, sb, k0, g.lda, wave);
     db.issue(rb, sb + BM * BKT, k0, g.ldb, wave);
   };
-  // raw barrier: the waits before it are explicit (__syncthreads would add vmcnt(0))
-  auto barrier = [&]() { asm volatile("s_barrier" ::: "memory"); };
+  // Raw barrier: the vector-memory waits before it are explicit (__syncthreads
+  // would add vmcnt(0) and drain the previous tile's stores). It waits for this
+  // wave's LDS reads itself: the compiler may place the MFMAs that consume a
+  // stage's last fragment reads after the barrier, and another wave's DMA into
+  // that stage buffer, issued right after it, could then overwrite fragments
+  // still being read. (Found as wrong output tiles of this kernel when an
+  // in-place CE kernel ran beside it on another stream.)
+  auto barrier = [&]() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
 
   constexpr int PITCH = 64 * (int)sizeof(OutT);  // one 32 x 64 slab per wave and store round
   constexpr int CPR = PITCH / 16;

@@ -238,3 +238,38 @@ def test_gemm_persistent_128_path_exact_small_integers(dev, opB, M, N, K, out):
     if out == "bf16":
         ref = torch.from_numpy(ref).bfloat16().float().numpy()
     assert np.array_equal(got, ref)
+
+
+def test_persistent_gemm_beside_inplace_ce_on_another_stream(dev):
+    """Regression: the persistent GEMM kernel's raw barriers once let a wave
+    pass with LDS fragment reads still pending, so another wave's DMA into the
+    same stage buffer could overwrite them. It showed as wrong 32- to 128-column
+    blocks of the output when an in-place CE ran beside the GEMM on another
+    stream (the LM head + CE in two chunks at 3000 rows: CE of rows [0, 1792)
+    beside the persistent 128 x 128 GEMM of rows [1792, 3000)). The GEMM beside
+    the CE must equal the GEMM alone, bit for bit, every time."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels import wgrad
+    from nlearn_amd.kernels.gemm import _ld, bf16_shadow, gemm_raw, padded_empty
+
+    M, V, cut = 3000, 50257, 1792
+    rng = np.random.default_rng(3)
+    X = torch.from_numpy(rng.standard_normal((M, 512)).astype(np.float32) * 0.5).to(dev).bfloat16()
+    W = torch.from_numpy(rng.standard_normal((512, V)).astype(np.float32) * 0.05).to(dev)
+    t = torch.from_numpy(rng.integers(0, V, M).astype(np.int32)).to(dev)
+    Wb = bf16_shadow(W)
+    alone = gemm_raw(X[cut:], Wb, out=padded_empty(M - cut, V, torch.bfloat16, dev))
+    main, aux = torch.cuda.current_stream(), wgrad._side_stream(dev, 1)
+    for _ in range(4):
+        logits = padded_empty(M, V, torch.bfloat16, dev)
+        loss, lse = torch.empty(M, device=dev), torch.empty(M, device=dev)
+        gemm_raw(X[:cut], Wb, out=logits[:cut])
+        aux.wait_stream(main)
+        with torch.cuda.stream(aux):
+            _lib.call("nl_ce_fwd_bwd", aux.cuda_stream, cut, V, logits.data_ptr(), _ld(logits), t.data_ptr(),
+                      loss.data_ptr(), lse.data_ptr(), 1.0 / M, logits.data_ptr(), _ld(logits))
+        gemm_raw(X[cut:], Wb, out=logits[cut:])
+        main.wait_stream(aux)
+        torch.cuda.synchronize()
+        assert torch.equal(logits[cut:], alone)
