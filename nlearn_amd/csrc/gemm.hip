@@ -458,10 +458,12 @@ __global__ __launch_bounds__((BM * BN >= 65536) ? 512 : 256,
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, b_bytes);
   // The 8-wave TN tile (the LM-head weight gradient) gives each stage's DMA
   // to half of its waves, alternating by stage (waves w and w + 4 share a
-  // SIMD). Issued by all 8 waves at once, the 64 KB queued behind a CU's
-  // ~28 B/clk global -> LDS path and blocked both waves of every SIMD for
-  // 800+ cycles per stage with the MFMA pipe idle; this way one of the two
-  // computes meanwhile. Measured at 512 x 50257 x 16384: 771-777 -> 737-744 us.
+  // SIMD). Issued by all 8 waves at once, the 64 instructions of a stage
+  // queue in the CU's memory pipeline, and both waves of every SIMD sat in
+  // the issue for 800+ cycles per stage with the MFMA pipe idle (the pipeline
+  // itself moves the 64 KB in about 0.8 us: the stall is the burst, not the
+  // bandwidth); this way one of the two computes meanwhile. Measured at
+  // 512 x 50257 x 16384: 771-777 -> 737-744 us.
   // (Slower for the NT form, 672-695 -> 694-708 us, and for 128 x 128 tiles.)
   constexpr int DNW = (!A_KMAJ && !B_KMAJ && kHuge && S == 2) ? NWV / 2 : NWV;
   Dma<BM, BKT, A_KMAJ, DNW> da;
@@ -1273,11 +1275,10 @@ Plan make_plan(int opA, int opB, int M, int N, int K, int epi) {
     p.tiles = (int)((int64_t)((M + 255) / 256) * ((N + 127) / 128));
   }
   // 256 x 256 tiles (8 waves of 128 x 64, 64-k stages) for products of
-  // >= 100 GFLOP without a fused epilogue (the LM head). Each CU then needs
-  // half the operand bytes per flop of a 128 x 128 tile: on MI355X the global
-  // -> LDS ingress of a CU saturates near 28 B/clk, which caps 128 x 128 tiles
-  // (64 B/clk at MFMA peak) well below 256 x 256 (32 B/clk). Measured at the
-  // LM-head shapes: NN 1076 -> 896 us, NT 1186 -> 897 us, TN 931 -> 811 us.
+  // >= 100 GFLOP without a fused epilogue (the LM head). Each CU then moves
+  // half the operand bytes, and issues half the DMA instructions and barriers,
+  // per flop of a 128 x 128 tile. Measured at the LM-head shapes: NN 1076 ->
+  // 896 us, NT 1186 -> 897 us, TN 931 -> 811 us.
   // One workgroup per CU, so a short grid splits K up to 256 workgroups.
   if (epi == NL_EPI_NONE && !(opA == NL_OP_T && opB == NL_OP_T) && 2.0 * M * N * K >= 1e11) {
     p.big = 2;
