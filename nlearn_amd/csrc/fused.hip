@@ -427,9 +427,15 @@ __global__ __launch_bounds__(256) void embed_count_kernel(int T, int vocab, int 
   __syncthreads();
   const int span = (T + kEmbParts - 1) / kEmbParts;
   const int t0 = k_part * span, t1 = min(T, t0 + span);
-  for (int t = t0 + tid; t < t1; t += 256) {
-    const int id = ids[t];
-    if ((uint32_t)id < (uint32_t)vocab) atomicAdd(&hist[id / W], 1);
+  // eight ids per thread loaded before any is counted: a load per increment
+  // made each thread a chain of dependent global loads
+  for (int c = t0 + tid; c < t1; c += 256 * 8) {
+    int v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = c + e * 256 < t1 ? ids[c + e * 256] : -1;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if ((uint32_t)v[e] < (uint32_t)vocab) atomicAdd(&hist[v[e] / W], 1);
   }
   __syncthreads();
   for (int b = tid; b < buckets; b += 256) counts[b * kEmbParts + k_part] = hist[b];
