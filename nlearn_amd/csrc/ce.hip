@@ -216,7 +216,15 @@ constexpr int kMeanBlock = 1024;
 __global__ __launch_bounds__(kMeanBlock) void mean_kernel(const float* __restrict__ x, int n, float* out) {
   __shared__ float sm[kMeanBlock / kWave];
   float acc = 0.f;
-  for (int i = threadIdx.x; i < n; i += kMeanBlock) acc += x[i];
+  // eight loads in flight per thread, added in the same order as one at a time
+  for (int i0 = threadIdx.x; i0 < n; i0 += 8 * kMeanBlock) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = i0 + e * kMeanBlock < n ? x[i0 + e * kMeanBlock] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (i0 + e * kMeanBlock < n) acc += v[e];
+  }
   acc = wave_sum(acc);
   if ((threadIdx.x & (kWave - 1)) == 0) sm[threadIdx.x / kWave] = acc;
   __syncthreads();
