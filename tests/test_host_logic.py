@@ -56,6 +56,19 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in r.stderr
 
 
+def test_bench_variant_failure_is_reported_not_raised(monkeypatch):
+    """A failure of the bs4 x seq4096 variant ends up in its detail entry, so
+    the headline JSON line is still printed."""
+    mod, _ = _bench_module()
+
+    def boom(*args, **kwargs):
+        raise RuntimeError("HIP out of memory")
+
+    monkeypatch.setattr(mod, "run_workload", boom)
+    got = mod.variant_detail(None, None, 50, 10, True, None)
+    assert got == {"error": "RuntimeError: HIP out of memory"}
+
+
 def test_busy_stats_counts_overlap_once():
     """The busy ratio is the union of kernel intervals over the replay window
     (from the first of the last `steps` step starts, marked by the embedding
