@@ -148,12 +148,11 @@ def test_colsum_exact_integers(dev, rows, cols):
 @pytest.mark.parametrize("M,N,K", [(1, 8, 16), (100, 1001, 70), (300, 520, 256), (512, 2048, 512),
                                    (256, 512, 4096), (4100, 4000, 256)])
 def test_gemm_bias_and_gelu_epilogues(dev, M, N, K, opB):
-    """Bias, bias+GELU and GELU' epilogues, exact on integer inputs. With B
-    stored [N, K] (opB "T", 64-k stages) and K a multiple of 64, the GELU'
-    epilogue's saved tile is fetched during the last K stage; K = 16 and 70
-    take the post-loop fetch; K = 4096 splits K (epilogue after the reduction);
-    (4100, 4000, 256) has enough tiles for the persistent kernel (bias and
-    bias + GELU epilogues, ragged edge tiles)."""
+    """Bias, bias+GELU and GELU' epilogues, exact on integer inputs, with B
+    stored [K, N] (opB "N") and [N, K] (opB "T"). K = 16 and 70 end in a ragged
+    K tail; K = 4096 splits K (epilogue after the reduction); (4100, 4000, 256)
+    has enough tiles for the persistent kernel (bias and bias + GELU
+    epilogues, ragged edge tiles)."""
     import torch
     from nlearn_amd.kernels.gemm import EPI_BIAS, EPI_BIAS_GELU, EPI_DGELU, gemm_raw, padded_empty
 
