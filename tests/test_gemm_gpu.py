@@ -159,6 +159,41 @@ def test_gemm_split_k_matches_single_pass_and_is_deterministic(dev, M, N, K):
     assert rel_l2(_np(split1[:, ct]), ops.gemm(_np(X), _np(dY[:, ct]), "T", "N")) <= 5e-3
 
 
+def test_gemm_ex_workspace_contract(dev):
+    """nl_gemm_ex splits K only when the workspace holds nl_gemm_ws_bytes: one
+    byte less (or none) gives the one-pass result, bit for bit that of nl_gemm;
+    the full size gives the split result, bit for bit that of gemm_raw."""
+    import torch
+    from nlearn_amd import _lib
+    from nlearn_amd.kernels.gemm import gemm_raw, padded_empty
+
+    M, N, K = 512, 1536, 16384
+    gen = torch.Generator(device=dev).manual_seed(21)
+    X = padded_empty(K, M, torch.bfloat16, dev)
+    X.copy_(torch.randn((K, M), generator=gen, device=dev))
+    dY = padded_empty(K, N, torch.bfloat16, dev)
+    dY.copy_(torch.randn((K, N), generator=gen, device=dev))
+    need = int(_lib.load().nl_gemm_ws_bytes(1, 0, M, N, K))
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    outs = {}
+    for name, wsb in (("none", 0), ("short", need - 1), ("full", need)):
+        c = padded_empty(M, N, torch.float32, dev)
+        _lib.call("nl_gemm_ex", st, 1, 0, M, N, K, 1.0, X.data_ptr(), X.stride(0), dY.data_ptr(), dY.stride(0), 0.0,
+                  c.data_ptr(), 0, c.stride(0), None, ws.data_ptr() if wsb else None, wsb)
+        outs[name] = c
+    single = padded_empty(M, N, torch.float32, dev)
+    _lib.call("nl_gemm", st, 1, 0, M, N, K, 1.0, X.data_ptr(), X.stride(0), dY.data_ptr(), dY.stride(0), 0.0,
+              single.data_ptr(), 0, single.stride(0), None)
+    split = gemm_raw(X, dY, "T", "N", out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(outs["none"], single)
+    assert torch.equal(outs["short"], single)
+    assert torch.equal(outs["full"], split)
+    assert rel_l2(_np(outs["full"]), _np(single)) <= 1e-5
+
+
 @pytest.mark.parametrize("opA,opB,M,N,K,out", [("N", "N", 2000, 9000, 3000, "f32"), ("N", "T", 4000, 600, 25000, "f32"),
                                                 ("T", "N", 600, 9000, 10000, "f32"), ("N", "N", 2000, 9000, 3000, "bf16"),
                                                 ("N", "N", 4000, 12000, 1152, "bf16"), ("N", "N", 4000, 12000, 1152, "f32"),
