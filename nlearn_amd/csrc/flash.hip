@@ -285,7 +285,8 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
   };
 
   const float c = a.scale_log2;  // scores are kept raw; exp2 arguments are c * s - m
-  float m = -INFINITY, l = 0.f;  // running max (scaled, log2 units) and this lane's partial sum
+  constexpr float kSlack = 8.f;
+  float m = -INFINITY, l = 0.f;  // exponent base (scaled, log2 units) and this lane's partial sum
   f32x16 o[2];
   zero(o[0]);
   zero(o[1]);
@@ -322,8 +323,14 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
     if (need_mask) mask_max(std::true_type{});
     else mask_max(std::false_type{});
     bm = fmaxf(bm, __shfl_xor(bm, 32, kWave));
-    const float mn = fmaxf(m, bm * c);
-    const float alpha = (m == -INFINITY) ? 0.f : fast_exp2(m - mn);
+    // The exponent base m moves only when the block max exceeds it by more
+    // than kSlack (log2 units). Probabilities then stay below 2^kSlack (bf16
+    // and fp32 hold them without loss of relative precision), and once the
+    // base has settled most blocks skip the rescale of O and l below.
+    const float cand = bm * c;
+    const bool up = cand > m + kSlack;
+    const float mn = up ? cand : m;
+    const float alpha = up ? ((m == -INFINITY) ? 0.f : fast_exp2(m - mn)) : 1.f;
     const float nmn = (mn == -INFINITY) ? 0.f : -mn;
     float rs = 0.f;
 #pragma unroll
@@ -336,8 +343,8 @@ __global__ __launch_bounds__(kThreads, 4) void flash_fwd_kernel(FwdArgs a) {
       }
     l = __builtin_fmaf(l, alpha, rs);
     m = mn;
-    // alpha == 1 exactly when the running max did not move; once the max has
-    // settled, whole blocks leave every row's max in place and skip the rescale
+    // alpha == 1 exactly when the base did not move: whole blocks then skip
+    // the rescale
     if (__ballot(alpha != 1.f)) {
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt)
