@@ -83,6 +83,37 @@ def test_flash_ragged_sequences(dev, B, H, S, causal):
     _check_against_oracle((O, L, dq, dk, dv), f32, B, H, S, causal)
 
 
+@pytest.mark.parametrize("B,H,S", [(1, 2, 545), (2, 1, 1024)])
+@pytest.mark.parametrize("causal", [True, False])
+def test_flash_scores_growing_along_the_keys(dev, B, H, S, causal):
+    """Scores that grow along the keys by about 45 log2 units over the
+    sequence: the forward's exponent base (which moves only when a block's
+    max exceeds it by more than 2^8) then moves several times after the first
+    block, with probabilities up to 2^8 in between, and O / l must still be
+    the softmax average. (Forward only: with |K| near 100 in one dimension,
+    dQ = scale * dS . K cancels heavily, since each row of dS sums to zero,
+    and bf16 dS is then outside the backward's tolerance on this data.)"""
+    import torch
+    from nlearn_amd.attention import flash_fwd_raw4
+
+    rng = np.random.default_rng(S + B)
+    q = rng.standard_normal((B, H, S, 64)).astype(np.float32)
+    k = rng.standard_normal((B, H, S, 64)).astype(np.float32)
+    q[..., 0] = 2.0 + np.abs(q[..., 0])                   # every query leans along dimension 0
+    k[..., 0] = 0.2 * np.arange(S, dtype=np.float32) * 544.0 / S   # later keys score higher
+    arrs = [ops.bf16_bits(a) for a in (q, k, rng.standard_normal((B, H, S, 64)).astype(np.float32))]
+    qd, kd, vd = (_dev_bf16(a, dev) for a in arrs)
+    qf, kf, vf = (ops.bf16_to_f32(a).reshape(B * H, S, 64) for a in arrs)
+    O, L = flash_fwd_raw4(qd, kd, vd, causal=causal)
+    torch.cuda.synchronize()
+    rO, rL = ops.flash_fwd(qf, kf, vf, causal=causal)
+    # the last query's scores really do grow by more than three moves of the base (log2 units)
+    growth = np.einsum("nd,nd->n", qf[:, -1], kf[:, -1] - kf[:, 0]) * 0.125 * math.log2(math.e)
+    assert growth.min() > 24.0
+    assert rel_l2(_np(O).reshape(B * H, S, 64), rO) <= TOL
+    assert np.abs(_np(L).reshape(B * H, S) - rL).max() <= 1e-2
+
+
 def test_flash_fused_qkv_layout_and_autograd(dev):
     """qkv (B, S, 3, H, D) consumed in place; O comes back as (B, S, H*D); the
     backward writes one (B, S, 3, H, D) gradient."""
